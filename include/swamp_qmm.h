@@ -1,0 +1,147 @@
+/*
+ * swamp_qmm.h -- C ABI of libswamp_gpu.so, the MI355X (gfx950) quantized
+ * matmul library for GGUF Q4_0 / Q8_0 / Q4_K weights.
+ *
+ * Conventions (all entry points):
+ *  - dtype codes are GGML's (swamp-gguf/src/dtype.rs:10-40):
+ *      SWAMP_F32 = 0, SWAMP_F16 = 1, SWAMP_Q4_0 = 2, SWAMP_Q8_0 = 8,
+ *      SWAMP_Q4_K = 12, SWAMP_BF16 = 30.
+ *  - W is row-major by output row, raw GGUF block bytes exactly as
+ *    GgufFile::tensor_raw_bytes returns them (swamp-gguf/src/mmap.rs:110-117):
+ *    row r starts at byte r * (n_cols / block) * type_size.
+ *    n_cols = tensor.shape[0] = K, n_rows = tensor.shape[1]
+ *    (swamp-engine/src/linear.rs:21-22).
+ *  - y[r] = sum_k W[r,k] * x[k] in fp32.
+ *  - Pointers named d_* are DEVICE pointers; the caller owns every buffer.
+ *  - stream is a hipStream_t passed as void* (NULL = default stream); every
+ *    device entry point is asynchronous on it and allocates nothing.
+ *  - Return 0 on success, a negative SWAMP_E* code on error; on error no
+ *    output is written and nothing is launched.
+ */
+#ifndef SWAMP_QMM_H
+#define SWAMP_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  SWAMP_F32 = 0,
+  SWAMP_F16 = 1,
+  SWAMP_Q4_0 = 2,
+  SWAMP_Q8_0 = 8,
+  SWAMP_Q4_K = 12,
+  SWAMP_BF16 = 30
+};
+
+enum {
+  SWAMP_OK = 0,
+  SWAMP_EINVAL = -1,    /* null pointer, negative size, misaligned pointer */
+  SWAMP_EDTYPE = -2,    /* dtype not supported by this entry point */
+  SWAMP_ESHAPE = -3,    /* n_cols not a multiple of the block, buffer too small */
+  SWAMP_ELAUNCH = -4,   /* HIP launch or copy failed */
+  SWAMP_ENODEVICE = -5, /* no HIP device */
+  SWAMP_EWORKSPACE = -6 /* workspace missing or too small */
+};
+
+/* Replaces gpu_init (swamp-gpu/src/lib.rs:62-71 -> fused_attention.cu:133-143)
+ * for the matmul library: selects the current device, creates its context
+ * and caches its CU count.  Idempotent; optional (every entry point calls
+ * it on first use). */
+int swamp_gpu_init(void);
+
+/* Text for a return code (static storage). */
+const char *swamp_strerror(int code);
+
+/* GgmlDType::block_size / type_size / nbytes_for (swamp-gguf/src/dtype.rs:
+ * 79-89, 92-132, 135-139).  0 for an unknown code. */
+size_t swamp_block_size(uint32_t dtype);
+size_t swamp_type_size(uint32_t dtype);
+size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
+
+/* quant::dequantize (swamp-gguf/src/quant/mod.rs:18-33) on the device, for
+ * F32, F16, BF16, Q4_0 (q4_0.rs:11-39), Q8_0 (q8_0.rs:15-40) and Q4_K
+ * (q4_k.rs:21-33, 278-321).  Writes n floats to d_dst, bit-identical to the
+ * reference's scalar CPU dequantizer (NaN inputs give NaN outputs).
+ * raw_len < nbytes_for(dtype, n) -> SWAMP_ESHAPE (the reference's
+ * BufferTooSmall, q4_0.rs:15-20). */
+int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
+                   float *d_dst, size_t n, void *stream);
+
+/* Decode GEMV, y = W x, OVERWRITING y[0..n_rows).
+ * Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the kernel
+ * it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:59-82).
+ * dtype Q4_0, Q8_0 or Q4_K; n_cols a multiple of the block size (32, or 256
+ * for Q4_K); w_len >= nbytes_for(dtype, n_rows * n_cols). */
+int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
+                const float *d_x, float *d_y, int n_rows, int n_cols,
+                void *stream);
+
+/* Several matrices that share one x (the engine's fused QKV and gate+up):
+ * y_m = W_m x for m < n_mats, each OVERWRITTEN, one launch.
+ * Replaces forward_linear_multi (linear.rs:96-170) and fused_gemv_q4k_multi
+ * (fused_gemv_q4k.rs:401-460).  All matrices share n_cols; dtypes may differ
+ * per matrix.  At most SWAMP_MULTI_MAX matrices. */
+#define SWAMP_MULTI_MAX 8
+int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
+                      const void *const *d_ws, const size_t *w_lens,
+                      const int *row_counts, const float *d_x,
+                      float *const *d_ys, int n_cols, void *stream);
+
+/* Small-batch GEMV/GEMM for speculative verify and continuous batching:
+ * n_tok tokens, d_x is [n_tok][n_cols] fp32, d_y is [n_tok][n_rows] fp32.
+ * accumulate = 0: y = W x (forward_linear_batch zeroes its outputs first,
+ * linear.rs:205-207); accumulate = 1: y += W x (the kernel contract of
+ * fused_gemv_q4k_batched, fused_gemv_q4k.rs:527-554, :694).
+ * Replaces forward_linear_batch (linear.rs:176-239) and
+ * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
+ * 16 tokens. */
+int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
+                        const float *d_x, float *d_y, int n_tok, int n_rows,
+                        int n_cols, int accumulate, void *stream);
+
+/* Prefill GEMM on the matrix cores: y[m][r] = sum_k W[r,k] x[m][k], fp32
+ * out [m][n_rows], OVERWRITTEN.  Replaces the prefill use of
+ * forward_linear_batch (swamp-engine/src/executor.rs:106-110 ->
+ * linear.rs:176-239).
+ *   x_type SWAMP_BF16: d_x is bf16 [m][n_cols]; W is dequantized into LDS
+ *     as bf16 and fed to bf16 MFMA (fp32 accumulate).
+ *   x_type SWAMP_Q8_0: d_x is Q8_0 blocks [m][n_cols/32] (as produced by
+ *     swamp_quantize_q8_0); int8 MFMA against W's int8 codes, fp32
+ *     per-block rescale.  Q4_0 and Q8_0 weights only.
+ * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only).  No workspace. */
+int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
+                const void *d_x, uint32_t x_type, float *d_y, int m,
+                int n_rows, int n_cols, void *stream);
+
+/* Activations to Q8_0 blocks on the device (the int8 GEMM's input):
+ * x_type SWAMP_F32 or SWAMP_BF16, n a multiple of 32, d_q receives
+ * n / 32 * 34 bytes.  Per block d = amax / 127 rounded to f16,
+ * q = round-half-away(x / d_unrounded) -- the block formula of the host
+ * quantizer swamp_quantize (swamp_quant.h). */
+int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n,
+                        void *stream);
+
+/* ---- the reference's two existing C exports, host-pointer semantics ---- */
+
+/* swamp_fused_gemv_q4k (fused_gemv_q4k.rs:799-823): HOST pointers, Q4_K,
+ * zeroes out and writes W x.  Null pointer or n_cols % 256 != 0 -> silent
+ * return, like the reference.  Stages through device memory on the current
+ * device and synchronizes before returning. */
+void swamp_fused_gemv_q4k(const uint8_t *w_raw, const float *x, float *out,
+                          int n_rows, int n_cols);
+
+/* swamp_gemv_q8_vnni (swamp-kernels/src/lib.rs:452-482): HOST pointers,
+ * exact int32 dot of two int8 vectors times scale; null or k <= 0 -> 0.0f.
+ * Computed on the device (staged), synchronizes before returning; returns
+ * NaN if the device step fails. */
+float swamp_gemv_q8_vnni(const int8_t *weights, const int8_t *activations,
+                         int k, float scale);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

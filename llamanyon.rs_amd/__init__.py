@@ -1,0 +1,231 @@
+"""ctypes binding of libswamp_gpu.so / libswamp_quant.so.
+
+Mirrors the loader of the reference's GPU bridge (swamp-gpu/src/lib.rs:30-54:
+one-time library load, symbol lookup, integer return codes mapped to an error
+type) for the quantized-matmul C ABI in include/swamp_qmm.h and the host
+quantizers in include/swamp_quant.h.  Device buffers are passed as integer
+addresses (for example torch.Tensor.data_ptr()); nothing here computes on the
+CPU except the host quantizers, which only prepare weight bytes.
+
+The directory name contains a dot, so import it by path:
+    spec = importlib.util.spec_from_file_location("llamanyon_rs_amd", ".../__init__.py")
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Sequence
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+GPU_LIB_PATH = os.path.join(PKG_DIR, "libswamp_gpu.so")
+QUANT_LIB_PATH = os.path.join(PKG_DIR, "libswamp_quant.so")
+
+# GGML dtype codes (swamp-gguf/src/dtype.rs:10-40)
+F32, F16, Q4_0, Q8_0, Q4_K, BF16 = 0, 1, 2, 8, 12, 30
+DTYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", BF16: "BF16"}
+BLOCK = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
+TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+
+# return codes (include/swamp_qmm.h)
+OK, EINVAL, EDTYPE, ESHAPE, ELAUNCH, ENODEVICE, EWORKSPACE = 0, -1, -2, -3, -4, -5, -6
+MULTI_MAX = 8
+
+# Every symbol include/swamp_qmm.h declares.
+GPU_SYMBOLS = (
+    "swamp_gpu_init", "swamp_strerror", "swamp_block_size", "swamp_type_size",
+    "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_multi",
+    "swamp_qgemv_batched", "swamp_qgemm", "swamp_quantize_q8_0",
+    "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
+)
+QUANT_SYMBOLS = (
+    "swamp_f32_to_f16", "swamp_f32_to_bf16", "swamp_f32_to_bf16_array",
+    "swamp_fill_normal", "swamp_quantize", "swamp_synth_quantized",
+)
+
+
+class GpuError(RuntimeError):
+    """GpuError::{LibLoad, Symbol, KernelError} of swamp-gpu/src/lib.rs:16-28."""
+
+    def __init__(self, code: int, what: str = ""):
+        self.code = code
+        super().__init__(f"{what}: error {code} ({strerror(code) if _gpu else 'library not loaded'})")
+
+
+_gpu: Optional[ctypes.CDLL] = None
+_quant: Optional[ctypes.CDLL] = None
+
+c_size = ctypes.c_size_t
+c_vp = ctypes.c_void_p
+
+
+def build(force: bool = False) -> None:
+    """Compile both libraries in-tree with the package Makefile."""
+    cmd = ["make", "-C", PKG_DIR, "-j8"]
+    if force:
+        subprocess.run(["make", "-C", PKG_DIR, "clean"], check=True, stdout=subprocess.DEVNULL)
+    subprocess.run(cmd, check=True)
+
+
+def gpu_lib() -> ctypes.CDLL:
+    """Load libswamp_gpu.so once (OnceLock semantics of swamp-gpu/src/lib.rs:30)."""
+    global _gpu
+    if _gpu is not None:
+        return _gpu
+    if not os.path.exists(GPU_LIB_PATH):
+        raise GpuError(ENODEVICE, f"{GPU_LIB_PATH} not built (run build())")
+    lib = ctypes.CDLL(GPU_LIB_PATH)
+    u32, i32 = ctypes.c_uint32, ctypes.c_int
+    sig = {
+        "swamp_gpu_init": (i32, []),
+        "swamp_strerror": (ctypes.c_char_p, [i32]),
+        "swamp_block_size": (c_size, [u32]),
+        "swamp_type_size": (c_size, [u32]),
+        "swamp_nbytes_for": (c_size, [u32, c_size]),
+        "swamp_qdequant": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp]),
+        "swamp_qgemv": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
+        "swamp_qgemv_multi": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
+                                    ctypes.POINTER(c_size), ctypes.POINTER(i32), c_vp,
+                                    ctypes.POINTER(c_vp), i32, c_vp]),
+        "swamp_qgemv_batched": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, i32, i32, c_vp]),
+        "swamp_qgemm": (i32, [u32, c_vp, c_size, c_vp, u32, c_vp, i32, i32, i32, c_vp]),
+        "swamp_quantize_q8_0": (i32, [c_vp, u32, c_vp, c_size, c_vp]),
+        "swamp_fused_gemv_q4k": (None, [c_vp, c_vp, c_vp, i32, i32]),
+        "swamp_gemv_q8_vnni": (ctypes.c_float, [c_vp, c_vp, i32, ctypes.c_float]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _gpu = lib
+    return lib
+
+
+def quant_lib() -> ctypes.CDLL:
+    global _quant
+    if _quant is not None:
+        return _quant
+    if not os.path.exists(QUANT_LIB_PATH):
+        raise GpuError(ENODEVICE, f"{QUANT_LIB_PATH} not built (run build())")
+    lib = ctypes.CDLL(QUANT_LIB_PATH)
+    u32, i32, u64 = ctypes.c_uint32, ctypes.c_int, ctypes.c_uint64
+    sig = {
+        "swamp_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+        "swamp_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+        "swamp_f32_to_bf16_array": (None, [c_vp, c_vp, c_size]),
+        "swamp_fill_normal": (i32, [u64, ctypes.c_float, c_vp, c_size, c_size, i32]),
+        "swamp_quantize": (i32, [u32, c_vp, c_vp, c_size, c_size, i32]),
+        "swamp_synth_quantized": (i32, [u32, u64, ctypes.c_float, c_vp, c_size, c_size, i32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _quant = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return gpu_lib().swamp_strerror(code).decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise GpuError(rc, what)
+
+
+def row_bytes(dtype: int, n_cols: int) -> int:
+    return n_cols // BLOCK[dtype] * TYPE_SIZE[dtype]
+
+
+def nbytes(dtype: int, n_rows: int, n_cols: int) -> int:
+    return n_rows * row_bytes(dtype, n_cols)
+
+
+# ---------------------------------------------------------------- device API
+
+def init() -> None:
+    _check(gpu_lib().swamp_gpu_init(), "swamp_gpu_init")
+
+
+def qdequant(dtype: int, d_raw: int, raw_len: int, d_dst: int, n: int, stream: int = 0) -> None:
+    _check(gpu_lib().swamp_qdequant(dtype, d_raw, raw_len, d_dst, n, stream), "swamp_qdequant")
+
+
+def qgemv(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_rows: int, n_cols: int,
+          stream: int = 0) -> None:
+    _check(gpu_lib().swamp_qgemv(dtype, d_w, w_len, d_x, d_y, n_rows, n_cols, stream), "swamp_qgemv")
+
+
+def qgemv_multi(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int],
+                row_counts: Sequence[int], d_x: int, d_ys: Sequence[int], n_cols: int,
+                stream: int = 0) -> None:
+    n = len(dtypes)
+    u32s = (ctypes.c_uint32 * n)(*dtypes)
+    ws = (c_vp * n)(*d_ws)
+    lens = (c_size * n)(*w_lens)
+    rows = (ctypes.c_int * n)(*row_counts)
+    ys = (c_vp * n)(*d_ys)
+    _check(gpu_lib().swamp_qgemv_multi(n, u32s, ws, lens, rows, d_x, ys, n_cols, stream),
+           "swamp_qgemv_multi")
+
+
+def qgemv_batched(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_tok: int,
+                  n_rows: int, n_cols: int, accumulate: bool = False, stream: int = 0) -> None:
+    _check(gpu_lib().swamp_qgemv_batched(dtype, d_w, w_len, d_x, d_y, n_tok, n_rows, n_cols,
+                                         1 if accumulate else 0, stream), "swamp_qgemv_batched")
+
+
+def qgemm(dtype: int, d_w: int, w_len: int, d_x: int, x_type: int, d_y: int, m: int,
+          n_rows: int, n_cols: int, stream: int = 0) -> None:
+    _check(gpu_lib().swamp_qgemm(dtype, d_w, w_len, d_x, x_type, d_y, m, n_rows, n_cols, stream),
+           "swamp_qgemm")
+
+
+def quantize_q8_0(d_x: int, x_type: int, d_q: int, n: int, stream: int = 0) -> None:
+    _check(gpu_lib().swamp_quantize_q8_0(d_x, x_type, d_q, n, stream), "swamp_quantize_q8_0")
+
+
+# ---------------------------------------------------------- host preparation
+
+def _np():
+    import numpy as np
+    return np
+
+
+def synth_quantized(dtype: int, seed: int, sigma: float, n_rows: int, n_cols: int,
+                    n_threads: int = 0):
+    """N(0, sigma^2) weights quantized to dtype blocks (numpy uint8 array)."""
+    np = _np()
+    out = np.empty(nbytes(dtype, n_rows, n_cols), dtype=np.uint8)
+    _check(quant_lib().swamp_synth_quantized(dtype, seed, sigma, out.ctypes.data, n_rows,
+                                             n_cols, n_threads), "swamp_synth_quantized")
+    return out
+
+
+def fill_normal(seed: int, sigma: float, n_rows: int, n_cols: int, n_threads: int = 0):
+    np = _np()
+    out = np.empty((n_rows, n_cols), dtype=np.float32)
+    _check(quant_lib().swamp_fill_normal(seed, sigma, out.ctypes.data, n_rows, n_cols, n_threads),
+           "swamp_fill_normal")
+    return out
+
+
+def quantize(dtype: int, src, n_threads: int = 0):
+    np = _np()
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    rows, cols = src.shape
+    out = np.empty(nbytes(dtype, rows, cols), dtype=np.uint8)
+    _check(quant_lib().swamp_quantize(dtype, src.ctypes.data, out.ctypes.data, rows, cols,
+                                      n_threads), "swamp_quantize")
+    return out
+
+
+def to_bf16_bits(src):
+    """float32 array -> uint16 bf16 bits (round to nearest even)."""
+    np = _np()
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.empty(src.shape, dtype=np.uint16)
+    quant_lib().swamp_f32_to_bf16_array(src.ctypes.data, out.ctypes.data, src.size)
+    return out

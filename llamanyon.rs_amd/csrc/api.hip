@@ -1,0 +1,275 @@
+// api.hip -- the C ABI of libswamp_gpu.so (declared in include/swamp_qmm.h).
+//
+// Validation and dispatch only; kernels live in dequant.hip, gemv.hip,
+// gemv_batched.hip and gemm.hip.  The error behaviour mirrors the
+// reference: shape asserts of fused_gemv_q4k (fused_gemv_q4k.rs:66-70) and
+// the bail! of forward_linear (linear.rs:23-25) become negative return
+// codes, checked before anything is launched; the two legacy host-pointer
+// exports keep their silent-return behaviour.
+#include <atomic>
+#include <mutex>
+#include <vector>
+
+#include "swamp_common.hpp"
+
+namespace swamp {
+
+namespace {
+constexpr int kMaxDevices = 64;
+DeviceInfo g_info[kMaxDevices];
+std::once_flag g_once[kMaxDevices];
+
+size_t block_size(uint32_t dt) {
+  switch (dt) {
+  case SWAMP_F32: case SWAMP_F16: case SWAMP_BF16: return 1;
+  case SWAMP_Q4_0: case SWAMP_Q8_0: return 32;
+  case SWAMP_Q4_K: return 256;
+  default: break;
+  }
+  // rest of the GgmlDType table (swamp-gguf/src/dtype.rs:79-89)
+  switch (dt) {
+  case 24: case 25: case 26: case 27: case 28: return 1;
+  case 3: case 6: case 7: case 9: case 20: case 23: return 32;
+  case 10: case 11: case 13: case 14: case 15: case 16: case 17: case 18:
+  case 19: case 21: case 22: case 29: return 256;
+  default: return 0;
+  }
+}
+
+size_t type_size(uint32_t dt) {
+  switch (dt) {  // swamp-gguf/src/dtype.rs:92-132
+  case 0: return 4;   case 1: return 2;   case 30: return 2;  case 28: return 8;
+  case 24: return 1;  case 25: return 2;  case 26: return 4;  case 27: return 8;
+  case 2: return 18;  case 3: return 20;  case 6: return 22;  case 7: return 24;
+  case 8: return 34;  case 9: return 40;  case 10: return 84; case 11: return 110;
+  case 12: return 144; case 13: return 176; case 14: return 210; case 15: return 292;
+  case 16: return 66; case 17: return 74; case 22: return 82; case 18: return 98;
+  case 21: return 110; case 20: return 18; case 23: return 136; case 19: return 50;
+  case 29: return 56;
+  default: return 0;
+  }
+}
+
+bool is_weight_dtype(uint32_t dt) {
+  return dt == SWAMP_Q4_0 || dt == SWAMP_Q8_0 || dt == SWAMP_Q4_K;
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Required base alignment of a weight buffer (dword vector loads; Q4_K
+// also loads its 16-byte headers as one vector).
+uintptr_t weight_align(uint32_t dt) { return dt == SWAMP_Q4_K ? 16 : 4; }
+
+int ensure_device(int *dev_out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return SWAMP_ENODEVICE;
+  if (dev < 0 || dev >= kMaxDevices) return SWAMP_ENODEVICE;
+  std::call_once(g_once[dev], [dev] {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+      g_info[dev].num_cus = cus;
+    g_info[dev].device = dev;
+  });
+  if (dev_out) *dev_out = dev;
+  return SWAMP_OK;
+}
+
+int check_gemv_args(uint32_t dtype, const void *d_w, size_t w_len, int n_rows, int n_cols) {
+  if (!is_weight_dtype(dtype)) return SWAMP_EDTYPE;
+  if (!d_w || n_rows < 0 || n_cols < 0) return SWAMP_EINVAL;
+  if (n_cols % int(block_size(dtype)) != 0) return SWAMP_ESHAPE;
+  if (!aligned(d_w, weight_align(dtype))) return SWAMP_EINVAL;
+  const size_t need = size_t(n_rows) * (size_t(n_cols) / block_size(dtype)) * type_size(dtype);
+  if (w_len < need) return SWAMP_ESHAPE;
+  return SWAMP_OK;
+}
+
+}  // namespace
+
+const DeviceInfo &device_info() {
+  int dev = 0;
+  ensure_device(&dev);
+  return g_info[dev];
+}
+
+}  // namespace swamp
+
+using namespace swamp;
+
+namespace {
+
+__global__ void i8dot_kernel(const int8_t *__restrict__ w, const int8_t *__restrict__ a, int k,
+                             int *__restrict__ out) {
+  // one workgroup of 256 lanes; exact int32 dot (the reference's scalar
+  // arm, swamp-kernels/src/lib.rs:477-481)
+  __shared__ int part[4];
+  int s = 0;
+  for (int i = threadIdx.x; i < k; i += blockDim.x) s += int(w[i]) * int(a[i]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = part[0] + part[1] + part[2] + part[3];
+}
+
+}  // namespace
+
+int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k, int *d_out, hipStream_t s) {
+  i8dot_kernel<<<1, 256, 0, s>>>(d_w, d_a, k, d_out);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
+
+extern "C" {
+
+int swamp_gpu_init(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return SWAMP_ENODEVICE;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return SWAMP_ENODEVICE;
+  if (hipSetDevice(dev) != hipSuccess) return SWAMP_ENODEVICE;
+  if (hipFree(nullptr) != hipSuccess) return SWAMP_ENODEVICE;  // create the context
+  return ensure_device(nullptr);
+}
+
+const char *swamp_strerror(int code) {
+  switch (code) {
+  case SWAMP_OK: return "ok";
+  case SWAMP_EINVAL: return "invalid argument (null, negative size or misaligned pointer)";
+  case SWAMP_EDTYPE: return "dtype not supported by this entry point";
+  case SWAMP_ESHAPE: return "shape mismatch (n_cols not a multiple of the block, or buffer too small)";
+  case SWAMP_ELAUNCH: return "HIP launch or copy failed";
+  case SWAMP_ENODEVICE: return "no HIP device";
+  case SWAMP_EWORKSPACE: return "workspace missing or too small";
+  default: return "unknown error";
+  }
+}
+
+size_t swamp_block_size(uint32_t dtype) { return block_size(dtype); }
+size_t swamp_type_size(uint32_t dtype) { return type_size(dtype); }
+size_t swamp_nbytes_for(uint32_t dtype, size_t n) {
+  const size_t bs = block_size(dtype);
+  return bs ? (n + bs - 1) / bs * type_size(dtype) : 0;
+}
+
+int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len, float *d_dst, size_t n,
+                   void *stream) {
+  const bool ok_dt = is_weight_dtype(dtype) || dtype == SWAMP_F32 || dtype == SWAMP_F16 ||
+                     dtype == SWAMP_BF16;
+  if (!ok_dt) return SWAMP_EDTYPE;
+  if (n == 0) return SWAMP_OK;
+  if (!d_raw || !d_dst) return SWAMP_EINVAL;
+  if (raw_len < swamp_nbytes_for(dtype, n)) return SWAMP_ESHAPE;
+  const uintptr_t al = dtype == SWAMP_Q4_K ? 16 : dtype == SWAMP_F32 ? 4 : 2;
+  if (!aligned(d_raw, al) || !aligned(d_dst, 4)) return SWAMP_EINVAL;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_dequant(dtype, d_raw, d_dst, n, static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x, float *d_y,
+                int n_rows, int n_cols, void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (!d_x || !d_y) return SWAMP_EINVAL;
+  if (!aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (n_rows == 0) return SWAMP_OK;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemv(dtype, d_w, d_x, d_y, n_rows, n_cols, static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
+                      const size_t *w_lens, const int *row_counts, const float *d_x,
+                      float *const *d_ys, int n_cols, void *stream) {
+  if (n_mats < 0 || n_mats > SWAMP_MULTI_MAX) return SWAMP_EINVAL;
+  if (n_mats == 0) return SWAMP_OK;
+  if (!dtypes || !d_ws || !w_lens || !row_counts || !d_ys || !d_x) return SWAMP_EINVAL;
+  if (!aligned(d_x, 16)) return SWAMP_EINVAL;
+  for (int i = 0; i < n_mats; i++) {
+    if (int rc = check_gemv_args(dtypes[i], d_ws[i], w_lens[i], row_counts[i], n_cols)) return rc;
+    if (!d_ys[i] || !aligned(d_ys[i], 4)) return SWAMP_EINVAL;
+  }
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemv_multi(n_mats, dtypes, d_ws, row_counts, d_x, d_ys, n_cols,
+                                 static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x,
+                        float *d_y, int n_tok, int n_rows, int n_cols, int accumulate,
+                        void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (n_tok < 0) return SWAMP_EINVAL;
+  if (n_tok == 0 || n_rows == 0) return SWAMP_OK;  // linear.rs:184
+  if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (dtype != SWAMP_Q4_K && n_cols % 64 != 0) return SWAMP_ESHAPE;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemv_batched(dtype, d_w, d_x, d_y, n_tok, n_rows, n_cols, accumulate ? 1 : 0,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, uint32_t x_type,
+                float *d_y, int m, int n_rows, int n_cols, void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (m < 0) return SWAMP_EINVAL;
+  if (x_type != SWAMP_BF16 && x_type != SWAMP_Q8_0) return SWAMP_EDTYPE;
+  if (x_type == SWAMP_Q8_0 && dtype == SWAMP_Q4_K) return SWAMP_EDTYPE;
+  if (m == 0 || n_rows == 0) return SWAMP_OK;
+  if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (n_cols % 64 != 0) return SWAMP_ESHAPE;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols,
+                           static_cast<hipStream_t>(stream));
+}
+
+int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n, void *stream) {
+  if (x_type != SWAMP_F32 && x_type != SWAMP_BF16) return SWAMP_EDTYPE;
+  if (n % 32 != 0) return SWAMP_ESHAPE;
+  if (n == 0) return SWAMP_OK;
+  if (!d_x || !d_q || !aligned(d_x, 4)) return SWAMP_EINVAL;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_quantize_q8_0(d_x, x_type, d_q, n, static_cast<hipStream_t>(stream));
+}
+
+void swamp_fused_gemv_q4k(const uint8_t *w_raw, const float *x, float *out, int n_rows,
+                          int n_cols) {
+  // fused_gemv_q4k.rs:799-823: null -> return; n_cols % 256 -> return; out
+  // zeroed then written.
+  if (!w_raw || !x || !out) return;
+  if (n_cols % 256 != 0 || n_rows < 0 || n_cols < 0) return;
+  if (ensure_device(nullptr) != SWAMP_OK) return;
+  const size_t wb = size_t(n_rows) * (size_t(n_cols) / 256) * 144;
+  void *dw = nullptr;
+  float *dx = nullptr, *dy = nullptr;
+  bool ok = hipMalloc(&dw, wb ? wb : 16) == hipSuccess &&
+            hipMalloc(reinterpret_cast<void **>(&dx), size_t(n_cols ? n_cols : 4) * 4) == hipSuccess &&
+            hipMalloc(reinterpret_cast<void **>(&dy), size_t(n_rows ? n_rows : 1) * 4) == hipSuccess;
+  if (ok) ok = hipMemcpy(dw, w_raw, wb, hipMemcpyHostToDevice) == hipSuccess &&
+               hipMemcpy(dx, x, size_t(n_cols) * 4, hipMemcpyHostToDevice) == hipSuccess;
+  for (int i = 0; i < n_rows; i++) out[i] = 0.0f;
+  if (ok && n_rows > 0 && n_cols > 0)
+    ok = swamp_launch_gemv(SWAMP_Q4_K, dw, dx, dy, n_rows, n_cols, nullptr) == SWAMP_OK &&
+         hipMemcpy(out, dy, size_t(n_rows) * 4, hipMemcpyDeviceToHost) == hipSuccess;
+  (void)hipFree(dw);
+  (void)hipFree(dx);
+  (void)hipFree(dy);
+}
+
+float swamp_gemv_q8_vnni(const int8_t *weights, const int8_t *activations, int k, float scale) {
+  if (!weights || !activations || k <= 0) return 0.0f;  // lib.rs:458
+  if (ensure_device(nullptr) != SWAMP_OK) return __builtin_nanf("");
+  int8_t *dw = nullptr, *da = nullptr;
+  int *dout = nullptr;
+  int dot = 0;
+  bool ok = hipMalloc(reinterpret_cast<void **>(&dw), size_t(k)) == hipSuccess &&
+            hipMalloc(reinterpret_cast<void **>(&da), size_t(k)) == hipSuccess &&
+            hipMalloc(reinterpret_cast<void **>(&dout), sizeof(int)) == hipSuccess;
+  if (ok) ok = hipMemcpy(dw, weights, size_t(k), hipMemcpyHostToDevice) == hipSuccess &&
+               hipMemcpy(da, activations, size_t(k), hipMemcpyHostToDevice) == hipSuccess &&
+               swamp_launch_i8dot(dw, da, k, dout, nullptr) == SWAMP_OK &&
+               hipMemcpy(&dot, dout, sizeof(int), hipMemcpyDeviceToHost) == hipSuccess;
+  (void)hipFree(dw);
+  (void)hipFree(da);
+  (void)hipFree(dout);
+  if (!ok) return __builtin_nanf("");
+  return float(dot) * scale;
+}
+
+}  // extern "C"

@@ -1,0 +1,180 @@
+// dequant.hip -- bit-exact device dequantization (quant::dequantize).
+//
+// This translation unit is compiled with -ffp-contract=off: the Q4_K value
+// (d*sc)*q - dmin*m must round the product and the difference separately,
+// as the reference's Rust does (swamp-gguf/src/quant/q4_k.rs:296-316).
+// Q4_0 and Q8_0 are one exact-integer-times-scale product each.
+//
+// Work split: one thread writes 8 consecutive outputs, so consecutive
+// threads store consecutive 32-byte runs (coalesced); the few block bytes
+// each thread needs are re-read by its neighbours from L1.
+#include "swamp_common.hpp"
+
+namespace {
+
+using swamp::f16_bits_to_f32_exact;
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+  return *reinterpret_cast<const uint16_t *>(p);
+}
+
+template <bool kVec>
+__device__ __forceinline__ void store8(float *dst, size_t base, size_t n,
+                                       const float (&v)[8]) {
+  if (kVec && base + 8 <= n) {
+    float4 *p = reinterpret_cast<float4 *>(dst + base);
+    p[0] = make_float4(v[0], v[1], v[2], v[3]);
+    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (base + j < n) dst[base + j] = v[j];
+  }
+}
+
+// q4_0::dequant (q4_0.rs:22-37): element i of a block is byte i/2, low
+// nibble for even i; value (nib - 8) * f16(d).
+template <bool kVec>
+__global__ void dequant_q4_0_kernel(const uint8_t *__restrict__ raw,
+                                    float *__restrict__ dst, size_t n) {
+  const size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t base = g * 8;
+  if (base >= n) return;
+  const size_t b = g >> 2;
+  const int t = int(g & 3);
+  const uint8_t *blk = raw + b * 18;
+  const float d = f16_bits_to_f32_exact(ld_u16(blk));
+  const uint32_t nib = ld_u16(blk + 2 + 4 * t) | (ld_u16(blk + 4 + 4 * t) << 16);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int q = int((nib >> (4 * j)) & 0xFu);  // byte j/2, low nibble first
+    v[j] = float(q - 8) * d;
+  }
+  store8<kVec>(dst, base, n, v);
+}
+
+// q8_0::dequant scalar arm (q8_0.rs:127-139): value int8 * f16(d).
+template <bool kVec>
+__global__ void dequant_q8_0_kernel(const uint8_t *__restrict__ raw,
+                                    float *__restrict__ dst, size_t n) {
+  const size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t base = g * 8;
+  if (base >= n) return;
+  const size_t b = g >> 2;
+  const int t = int(g & 3);
+  const uint8_t *blk = raw + b * 34;
+  const float d = f16_bits_to_f32_exact(ld_u16(blk));
+  const uint8_t *qs = blk + 2 + 8 * t;
+  const uint32_t lo = ld_u16(qs) | (ld_u16(qs + 2) << 16);
+  const uint32_t hi = ld_u16(qs + 4) | (ld_u16(qs + 6) << 16);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    v[j] = float(int8_t(uint8_t(lo >> (8 * j)))) * d;
+    v[4 + j] = float(int8_t(uint8_t(hi >> (8 * j)))) * d;
+  }
+  store8<kVec>(dst, base, n, v);
+}
+
+// q4_k::dequant_scalar (q4_k.rs:278-321) with unpack_scales (:37-53),
+// layout A: pair p = sub-blocks (2p, 2p+1) use qs[32p..32p+32], low nibble
+// for the even sub-block, high nibble for the odd one.
+template <bool kVec>
+__global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ raw,
+                                    float *__restrict__ dst, size_t n) {
+  const size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t base = g * 8;
+  if (base >= n) return;
+  const size_t b = g >> 5;
+  const int e0 = int(g & 31) * 8;  // first element within the super-block
+  const int sb = e0 >> 5;          // sub-block 0..7
+  const int i0 = e0 & 31;
+  const int pair = sb >> 1;
+  const bool high = sb & 1;
+  const uint8_t *blk = raw + b * 144;
+  const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+  const float d = f16_bits_to_f32_exact(hdr.x & 0xFFFFu);
+  const float dmin = f16_bits_to_f32_exact(hdr.x >> 16);
+  // 12 scale bytes: sc[0..3] = hdr.y, sc[4..7] = hdr.z, sc[8..11] = hdr.w
+  const uint32_t s03 = hdr.y, s47 = hdr.z, s811 = hdr.w;
+  uint32_t scale, mn;
+  if (sb < 4) {
+    scale = (s03 >> (8 * sb)) & 63u;
+    mn = (s47 >> (8 * sb)) & 63u;
+  } else {
+    const int j = sb - 4;
+    const uint32_t b8 = (s811 >> (8 * j)) & 0xFFu;        // sc[j+8]
+    const uint32_t bj = (s03 >> (8 * j)) & 0xFFu;         // sc[j]
+    const uint32_t bj4 = (s47 >> (8 * j)) & 0xFFu;        // sc[j+4]
+    scale = (b8 & 0xFu) | ((bj >> 6) << 4);
+    mn = (b8 >> 4) | ((bj4 >> 6) << 4);
+  }
+  const float sv = d * float(scale & 0x3Fu);
+  const float mv = dmin * float(mn & 0x3Fu);
+  const uint2 q = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * pair + i0);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t byte = ((j < 4 ? q.x : q.y) >> (8 * (j & 3))) & 0xFFu;
+    const uint32_t qi = high ? (byte >> 4) : (byte & 0xFu);
+    const float t = sv * float(qi);
+    v[j] = t - mv;
+  }
+  store8<kVec>(dst, base, n, v);
+}
+
+__global__ void dequant_f16_kernel(const uint16_t *__restrict__ raw,
+                                   float *__restrict__ dst, size_t n) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = f16_bits_to_f32_exact(raw[i]);
+}
+
+__global__ void dequant_bf16_kernel(const uint16_t *__restrict__ raw,
+                                    float *__restrict__ dst, size_t n) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = __uint_as_float(uint32_t(raw[i]) << 16);
+}
+
+template <template <bool> class K>
+struct Dummy {};
+
+}  // namespace
+
+int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
+                         size_t n, hipStream_t s) {
+  if (n == 0) return SWAMP_OK;
+  const int threads = 256;
+  const bool vec = (reinterpret_cast<uintptr_t>(d_dst) & 15u) == 0;
+  const uint8_t *raw = static_cast<const uint8_t *>(d_raw);
+  const size_t groups = (n + 7) / 8;
+  const dim3 grid8(unsigned((groups + threads - 1) / threads));
+  const dim3 grid1(unsigned((n + threads - 1) / threads));
+  switch (dtype) {
+  case SWAMP_Q4_0:
+    if (vec) dequant_q4_0_kernel<true><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    else dequant_q4_0_kernel<false><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    break;
+  case SWAMP_Q8_0:
+    if (vec) dequant_q8_0_kernel<true><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    else dequant_q8_0_kernel<false><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    break;
+  case SWAMP_Q4_K:
+    if (vec) dequant_q4_k_kernel<true><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    else dequant_q4_k_kernel<false><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    break;
+  case SWAMP_F16:
+    dequant_f16_kernel<<<grid1, threads, 0, s>>>(static_cast<const uint16_t *>(d_raw), d_dst, n);
+    break;
+  case SWAMP_BF16:
+    dequant_bf16_kernel<<<grid1, threads, 0, s>>>(static_cast<const uint16_t *>(d_raw), d_dst, n);
+    break;
+  case SWAMP_F32:
+    if (hipMemcpyAsync(d_dst, d_raw, n * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return SWAMP_ELAUNCH;
+    return SWAMP_OK;
+  default:
+    return SWAMP_EDTYPE;
+  }
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}

@@ -1,0 +1,112 @@
+// swamp_common.hpp -- shared device/host helpers for libswamp_gpu.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "swamp_qmm.h"
+
+namespace swamp {
+
+// Block geometry of the three weight formats (swamp-gguf/src/dtype.rs:79-132).
+constexpr int kQ4_0Block = 32, kQ4_0Bytes = 18;
+constexpr int kQ8_0Block = 32, kQ8_0Bytes = 34;
+constexpr int kQ4_KBlock = 256, kQ4_KBytes = 144;
+
+// One "item" is 64 consecutive weights of one row: two Q4_0 blocks (36 B),
+// two Q8_0 blocks (68 B) or one quarter of a Q4_K super-block (32 nibble
+// bytes plus the block's 16-byte header).  Every kernel that streams rows
+// hands out whole items to lanes.
+constexpr int kItem = 64;
+
+__host__ __device__ constexpr int item_bytes(int dt) {
+  return dt == SWAMP_Q4_0 ? 36 : dt == SWAMP_Q8_0 ? 68 : 36 /* Q4_K: 144/4 */;
+}
+
+__host__ __device__ constexpr size_t row_bytes(int dt, size_t n_cols) {
+  return dt == SWAMP_Q4_0   ? n_cols / 32 * 18
+         : dt == SWAMP_Q8_0 ? n_cols / 32 * 34
+         : dt == SWAMP_Q4_K ? n_cols / 256 * 144
+                            : 0;
+}
+
+// 16-byte load with 4-byte alignment (gfx950 global loads accept dword
+// alignment for multi-dword accesses).
+struct __attribute__((aligned(4))) u32x4 {
+  uint32_t v[4];
+};
+
+__device__ __forceinline__ u32x4 ld4(const uint8_t *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ uint32_t ld1(const uint8_t *p) {
+  return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// Exact binary16 -> binary32 in integer arithmetic (same rules as
+// half::f16::to_f32: subnormals renormalised, NaN payload kept + quiet bit).
+__device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t man = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {
+      // man has its leading one at bit p (0..9); value = man * 2^-24.
+      const int p = 31 - __builtin_clz(man);
+      bits = sign | (uint32_t(p + 103) << 23) | ((man << (23 - p)) & 0x7FFFFFu);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (man ? (0x400000u | (man << 13)) : 0u);
+  } else {
+    bits = sign | ((exp + 112u) << 23) | (man << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+// Hardware conversion (v_cvt_f32_f16); exact for every finite input.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, uint16_t(h & 0xFFFFu));
+  return float(v);
+}
+
+// Wavefront (64-lane) sum; result valid in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Per-device properties cached by the host side.
+struct DeviceInfo {
+  int device = -1;
+  int num_cus = 256;
+};
+const DeviceInfo &device_info();  // current device (initialises it)
+
+}  // namespace swamp
+
+// Internal launchers (defined in dequant.hip, gemv.hip, gemm.hip).  They
+// assume the arguments have been validated by api.cpp.
+int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
+                         size_t n, hipStream_t s);
+int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x,
+                      float *d_y, int n_rows, int n_cols, hipStream_t s);
+int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes,
+                            const void *const *d_ws, const int *row_counts,
+                            const float *d_x, float *const *d_ys, int n_cols,
+                            hipStream_t s);
+int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,
+                              const float *d_x, float *d_y, int n_tok,
+                              int n_rows, int n_cols, int accumulate,
+                              hipStream_t s);
+int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x,
+                      uint32_t x_type, float *d_y, int m, int n_rows,
+                      int n_cols, hipStream_t s);
+int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q,
+                               size_t n, hipStream_t s);
+int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k,
+                       int *d_out, hipStream_t s);

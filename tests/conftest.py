@@ -1,0 +1,50 @@
+"""Shared fixtures: the product package (loaded by path: its directory name
+has a dot) and the oracle wrapper (test infrastructure)."""
+import importlib.util
+import os
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+
+def _load(name, path):
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def load_pkg():
+    return _load("llamanyon_rs_amd", os.path.join(REPO, "llamanyon.rs_amd", "__init__.py"))
+
+
+def load_oracle():
+    return _load("swamp_oracle_py", os.path.join(REPO, "oracle", "oracle.py"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X / gfx950)")
+
+
+@pytest.fixture(scope="session")
+def pkg():
+    return load_pkg()
+
+
+@pytest.fixture(scope="session")
+def orc():
+    return load_oracle()
+
+
+@pytest.fixture(scope="session")
+def fixtures():
+    import json
+    with open(os.path.join(REPO, "tests", "golden", "fixtures.json")) as f:
+        return json.load(f)

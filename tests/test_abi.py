@@ -1,0 +1,99 @@
+"""The C ABI: both libraries load, export every function include/*.h
+declares, and reject bad arguments before touching a device.  CPU only (no
+compute call is made)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared(header):
+    text = open(os.path.join(REPO, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(swamp_[a-z0-9_]+)\s*\(", text)))
+
+
+def exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_gpu_lib_exports_header(pkg):
+    names = declared("swamp_qmm.h")
+    assert set(names) == set(pkg.GPU_SYMBOLS)
+    syms = exported(pkg.GPU_LIB_PATH)
+    missing = [n for n in names if n not in syms]
+    assert not missing, missing
+    pkg.gpu_lib()  # dlopen + every signature binds
+
+
+def test_quant_lib_exports_header(pkg):
+    names = declared("swamp_quant.h")
+    assert set(names) == set(pkg.QUANT_SYMBOLS)
+    syms = exported(pkg.QUANT_LIB_PATH)
+    assert not [n for n in names if n not in syms]
+
+
+def test_gpu_lib_has_gfx950_code(pkg):
+    # the embedded offload bundle names its targets; only gfx950 is built
+    data = open(pkg.GPU_LIB_PATH, "rb").read()
+    targets = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx[0-9a-z]+)", data))
+    assert targets == {b"gfx950"}
+
+
+def test_dtype_table_matches_oracle(pkg, orc):
+    L, O = pkg.gpu_lib(), orc.lib()
+    for code in list(range(0, 31)) + [99]:
+        assert L.swamp_block_size(code) == O.or_block_size(code), code
+        assert L.swamp_type_size(code) == O.or_type_size(code), code
+        for n in (0, 1, 31, 32, 33, 256, 257, 4096 * 4096):
+            assert L.swamp_nbytes_for(code, n) == O.or_nbytes_for(code, n)
+
+
+def test_strerror(pkg):
+    for code in (0, -1, -2, -3, -4, -5, -6, -77):
+        assert isinstance(pkg.strerror(code), str) and pkg.strerror(code)
+
+
+def test_argument_validation_precedes_device(pkg):
+    L = pkg.gpu_lib()
+    fake = 0x10000  # never dereferenced: every call below fails validation
+    # unsupported dtype (Q6_K = 14)
+    assert L.swamp_qgemv(14, fake, 1 << 20, fake, fake, 4, 256, None) == pkg.EDTYPE
+    # n_cols not a multiple of the block
+    assert L.swamp_qgemv(pkg.Q4_K, fake, 1 << 20, fake, fake, 4, 255, None) == pkg.ESHAPE
+    assert L.swamp_qgemv(pkg.Q4_0, fake, 1 << 20, fake, fake, 4, 48, None) == pkg.ESHAPE
+    # weight buffer too small (BufferTooSmall / length assert)
+    assert L.swamp_qgemv(pkg.Q4_0, fake, 100, fake, fake, 4, 64, None) == pkg.ESHAPE
+    # null / misaligned
+    assert L.swamp_qgemv(pkg.Q4_0, None, 1 << 20, fake, fake, 4, 64, None) == pkg.EINVAL
+    assert L.swamp_qgemv(pkg.Q4_K, fake + 4, 1 << 20, fake, fake, 4, 256, None) == pkg.EINVAL
+    assert L.swamp_qgemv(pkg.Q4_0, fake, 1 << 20, fake + 4, fake, 4, 64, None) == pkg.EINVAL
+    assert L.swamp_qgemv_batched(pkg.Q4_0, fake, 1 << 20, fake, fake, -1, 4, 64, 0, None) == pkg.EINVAL
+    assert L.swamp_qgemm(pkg.Q4_K, fake, 1 << 20, fake, pkg.Q8_0, fake, 4, 4, 256, None) == pkg.EDTYPE
+    assert L.swamp_qgemm(pkg.Q4_0, fake, 1 << 20, fake, pkg.F16, fake, 4, 4, 64, None) == pkg.EDTYPE
+    assert L.swamp_qdequant(14, fake, 1 << 20, fake, 64, None) == pkg.EDTYPE
+    assert L.swamp_qdequant(pkg.Q4_0, fake, 35, fake, 64, None) == pkg.ESHAPE
+    assert L.swamp_quantize_q8_0(fake, pkg.F32, fake, 33, None) == pkg.ESHAPE
+    n = 9
+    dts = (ctypes.c_uint32 * n)(*([pkg.Q4_0] * n))
+    assert L.swamp_qgemv_multi(n, dts, None, None, None, fake, None, 64, None) == pkg.EINVAL
+
+
+def test_legacy_exports_null_behaviour(pkg):
+    L = pkg.gpu_lib()
+    # swamp_gemv_q8_vnni: null or k <= 0 -> 0.0 (lib.rs:458)
+    assert L.swamp_gemv_q8_vnni(None, None, 64, 1.0) == 0.0
+    buf = np.zeros(8, np.int8)
+    assert L.swamp_gemv_q8_vnni(buf.ctypes.data, buf.ctypes.data, 0, 1.0) == 0.0
+    # swamp_fused_gemv_q4k: null -> silent return; n_cols % 256 -> silent return
+    out = np.full(4, 7.0, np.float32)
+    L.swamp_fused_gemv_q4k(None, None, out.ctypes.data, 4, 256)
+    L.swamp_fused_gemv_q4k(buf.ctypes.data, buf.ctypes.data, out.ctypes.data, 4, 100)
+    assert out.tolist() == [7.0] * 4

@@ -1,0 +1,347 @@
+"""GPU parity: every entry point of libswamp_gpu.so against the CPU oracle on
+identical seeded inputs.  Gates (from the path's contract):
+  * dequantization is bit-identical (NaN positions identical);
+  * matmul outputs satisfy max_r |y - y_ref| / (||W_r|| ||x||) <= 1e-3, with
+    W the oracle-dequantized weights and x the activations actually fed
+    (bf16-rounded for the prefill GEMM).
+Large shapes run on the GPU in full; the oracle checks row/token subsets
+and the size-independent properties (linearity, batch = per-token)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, F32, F16, BF16 = 2, 8, 12, 0, 1, 30
+TOL = 1e-3
+SEED = 0x5EED
+
+
+@pytest.fixture(scope="module")
+def torch_dev(pkg):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    pkg.init()
+    return torch
+
+
+def up(torch, arr):
+    t = torch.from_numpy(np.ascontiguousarray(arr)).cuda()
+    return t
+
+
+def down(t):
+    return t.cpu().numpy()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def say(*a):
+    print("[gpu case]", *a, flush=True)
+
+
+def weights(pkg, dtype, rows, cols, mid=0, sigma=0.02):
+    return pkg.synth_quantized(dtype, SEED ^ (7 << 32) ^ mid, sigma, rows, cols)
+
+
+def acts(pkg, n, cols, mid=0):
+    return pkg.fill_normal(SEED ^ 0xA11CE ^ mid, 1.0, n, cols)
+
+
+# ------------------------------------------------------------------ dequant
+
+def _same_bits(a, b):
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype,n", [(Q4_0, 32), (Q4_0, 4096 * 4096), (Q4_0, 1000), (Q4_0, 7),
+                                     (Q8_0, 4096 * 1024), (Q8_0, 999),
+                                     (Q4_K, 256), (Q4_K, 4096 * 1024), (Q4_K, 300)])
+def test_dequant_bit_exact(pkg, orc, torch_dev, dtype, n):
+    torch = torch_dev
+    cols = 256 if dtype == Q4_K else 32
+    blocks_n = (n + cols - 1) // cols * cols
+    raw = weights(pkg, dtype, 1, blocks_n, mid=n)
+    say("dequant", dtype, n)
+    d_raw = up(torch, raw)
+    d_out = torch.empty(n, dtype=torch.float32, device="cuda")
+    pkg.qdequant(dtype, d_raw.data_ptr(), raw.size, d_out.data_ptr(), n, stream(torch))
+    torch.cuda.synchronize()
+    assert _same_bits(down(d_out), orc.dequantize(dtype, raw, n))
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+def test_dequant_random_bytes_bit_exact(pkg, orc, torch_dev, dtype):
+    """Uniformly random block bytes: every f16 scale code (subnormal, inf,
+    NaN) and every 6-bit scale/min code appear."""
+    torch = torch_dev
+    bs, ts = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}[dtype]
+    nblk = 20000
+    raw = np.random.default_rng(dtype).integers(0, 256, nblk * ts, dtype=np.uint8)
+    n = nblk * bs
+    say("dequant random bytes", dtype)
+    d_raw = up(torch, raw)
+    d_out = torch.empty(n, dtype=torch.float32, device="cuda")
+    pkg.qdequant(dtype, d_raw.data_ptr(), raw.size, d_out.data_ptr(), n, stream(torch))
+    torch.cuda.synchronize()
+    assert _same_bits(down(d_out), orc.dequantize(dtype, raw, n))
+
+
+def test_dequant_every_f16_scale(pkg, orc, torch_dev):
+    """Q8_0 blocks with d = each of the 65536 f16 codes and q = 1: the device
+    f16 decode equals the oracle's for every code."""
+    torch = torch_dev
+    codes = np.arange(65536, dtype=np.uint16)
+    raw = np.zeros((65536, 34), dtype=np.uint8)
+    raw[:, 0] = codes & 0xFF
+    raw[:, 1] = codes >> 8
+    raw[:, 2:] = 1
+    raw = raw.reshape(-1)
+    n = 65536 * 32
+    say("dequant every f16 code")
+    d_raw = up(torch, raw)
+    d_out = torch.empty(n, dtype=torch.float32, device="cuda")
+    pkg.qdequant(Q8_0, d_raw.data_ptr(), raw.size, d_out.data_ptr(), n, stream(torch))
+    torch.cuda.synchronize()
+    assert _same_bits(down(d_out), orc.dequantize(Q8_0, raw, n))
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16, F32])
+def test_dequant_float_types(pkg, orc, torch_dev, dtype):
+    torch = torch_dev
+    n = 70001
+    raw = np.random.default_rng(5).integers(0, 256, n * (4 if dtype == F32 else 2), dtype=np.uint8)
+    d_raw = up(torch, raw)
+    d_out = torch.empty(n, dtype=torch.float32, device="cuda")
+    pkg.qdequant(dtype, d_raw.data_ptr(), raw.size, d_out.data_ptr(), n, stream(torch))
+    torch.cuda.synchronize()
+    assert _same_bits(down(d_out), orc.dequantize(dtype, raw, n))
+
+
+# --------------------------------------------------------------------- GEMV
+
+def _gemv_check(pkg, orc, torch, dtype, rows, cols, check_rows=None, mid=0):
+    raw = weights(pkg, dtype, rows, cols, mid=mid)
+    x = acts(pkg, 1, cols, mid=mid)[0]
+    say("gemv", dtype, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, x)
+    d_y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), rows, cols,
+              stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.all(np.isfinite(y))
+    rb = pkg.row_bytes(dtype, cols)
+    sel = check_rows if check_rows is not None else [(0, rows)]
+    worst = 0.0
+    for r0, r1 in sel:
+        sub = raw[r0 * rb:r1 * rb]
+        ref = orc.forward_linear(dtype, sub, x, r1 - r0, cols, 8)
+        deq = orc.dequantize(dtype, sub, (r1 - r0) * cols).reshape(r1 - r0, cols)
+        worst = max(worst, orc.normalized_error(y[r0:r1], ref, deq, x))
+    assert worst <= TOL, worst
+    return worst
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (37, 4096), (1, 256), (4096, 14336),
+                                       (300, 28672), (64, 65536)])
+def test_gemv_parity(pkg, orc, torch_dev, dtype, rows, cols):
+    _gemv_check(pkg, orc, torch_dev, dtype, rows, cols)
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("cols", [64, 320, 96, 4064])
+def test_gemv_parity_small_blocks(pkg, orc, torch_dev, dtype, cols):
+    # n_cols % 64 != 0 takes the generic one-block-per-lane kernel
+    _gemv_check(pkg, orc, torch_dev, dtype, 129, cols)
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q4_K])
+def test_gemv_8b_shapes_subsets(pkg, orc, torch_dev, dtype):
+    for rows, cols in [(6144, 4096), (28672, 4096), (128256, 4096)]:
+        _gemv_check(pkg, orc, torch_dev, dtype, rows, cols,
+                    check_rows=[(0, 1024), (rows // 2, rows // 2 + 512), (rows - 1024, rows)])
+
+
+def test_gemv_linearity_full_lm_head(pkg, torch_dev):
+    """Size-independent check at the full lm_head shape: W(2x) = 2 Wx and
+    W(x1 + x2) ~ Wx1 + Wx2."""
+    torch = torch_dev
+    rows, cols = 128256, 4096
+    raw = weights(pkg, Q8_0, rows, cols, mid=99)
+    x = acts(pkg, 2, cols, mid=99)
+    d_w = up(torch, raw)
+    outs = []
+    for v in (x[0], 2 * x[0], x[1], x[0] + x[1]):
+        d_x = up(torch, v.astype(np.float32))
+        d_y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        pkg.qgemv(Q8_0, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), rows, cols,
+                  stream(torch))
+        outs.append(down(d_y))
+    torch.cuda.synchronize()
+    assert np.array_equal(outs[1], 2 * outs[0])
+    scale = np.abs(outs[0]).max() + np.abs(outs[2]).max()
+    assert np.abs(outs[3] - (outs[0] + outs[2])).max() <= 1e-4 * scale
+
+
+def test_gemv_multi(pkg, orc, torch_dev):
+    torch = torch_dev
+    cols = 4096
+    spec = [(Q4_0, 4096), (Q4_0, 1024), (Q4_0, 1024), (Q4_K, 333), (Q8_0, 77)]
+    raws = [weights(pkg, dt, r, cols, mid=i) for i, (dt, r) in enumerate(spec)]
+    x = acts(pkg, 1, cols, mid=5)[0]
+    d_ws = [up(torch, r) for r in raws]
+    d_ys = [torch.empty(r, dtype=torch.float32, device="cuda") for _, r in spec]
+    d_x = up(torch, x)
+    say("gemv multi")
+    pkg.qgemv_multi([dt for dt, _ in spec], [t.data_ptr() for t in d_ws], [r.size for r in raws],
+                    [r for _, r in spec], d_x.data_ptr(), [t.data_ptr() for t in d_ys], cols,
+                    stream(torch))
+    torch.cuda.synchronize()
+    for (dt, r), raw, d_y in zip(spec, raws, d_ys):
+        ref = orc.forward_linear(dt, raw, x, r, cols, 8)
+        deq = orc.dequantize(dt, raw, r * cols).reshape(r, cols)
+        assert orc.normalized_error(down(d_y), ref, deq, x) <= TOL
+
+
+# ------------------------------------------------------------ small batch
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19])
+@pytest.mark.parametrize("rows,cols", [(1000, 4096), (256, 14336)])
+def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
+    torch = torch_dev
+    raw = weights(pkg, dtype, rows, cols, mid=n_tok)
+    xs = acts(pkg, n_tok, cols, mid=n_tok)
+    say("batched", dtype, n_tok, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, xs)
+    d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv_batched(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                      rows, cols, False, stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    ref = orc.forward_linear_batch(dtype, raw, xs, rows, cols, 8)
+    deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(y, ref, deq, xs) <= TOL
+
+
+@pytest.mark.parametrize("cols", [4096, 14336])
+def test_batched_accumulate(pkg, orc, torch_dev, cols):
+    """accumulate=1 is the kernel contract of fused_gemv_q4k_batched
+    (out += W x, fused_gemv_q4k.rs:694)."""
+    torch = torch_dev
+    rows, n_tok = 512, 6
+    raw = weights(pkg, Q4_K, rows, cols, mid=3)
+    xs = acts(pkg, n_tok, cols, mid=3)
+    base = np.random.default_rng(1).standard_normal((n_tok, rows)).astype(np.float32)
+    d_w, d_x, d_y = up(torch, raw), up(torch, xs), up(torch, base)
+    pkg.qgemv_batched(Q4_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok, rows,
+                      cols, True, stream(torch))
+    torch.cuda.synchronize()
+    outs = base.copy()
+    orc.fused_gemv_q4k_batched(raw, xs, outs, rows, cols)
+    deq = orc.dequantize(Q4_K, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(down(d_y), outs, deq, xs) <= TOL
+
+
+# ------------------------------------------------------------ prefill GEMM
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("m,rows,cols", [(512, 4096, 4096), (77, 300, 1024), (2048, 512, 4096),
+                                         (256, 1024, 14336)])
+def test_gemm_bf16_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
+    torch = torch_dev
+    raw = weights(pkg, dtype, rows, cols, mid=m)
+    x = acts(pkg, m, cols, mid=m)
+    xb = pkg.to_bf16_bits(x)
+    x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
+    say("gemm bf16", dtype, m, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, xb.view(np.int16))
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), BF16, d_y.data_ptr(), m, rows,
+              cols, stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.all(np.isfinite(y))
+    toks = sorted(set([0, 1, m // 2, m - 1] + list(range(max(0, m - 3), m))))
+    ref = orc.forward_linear_batch(dtype, raw, x_fed[toks], rows, cols, 8)
+    deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(y[toks], ref, deq, x_fed[toks]) <= TOL
+
+
+def test_gemm_rows_tail_and_token_consistency(pkg, orc, torch_dev):
+    """GEMM token rows equal the per-token GEMV within tolerance; a ragged
+    row count (not a tile multiple) leaves no NaN."""
+    torch = torch_dev
+    m, rows, cols = 300, 777, 2048
+    raw = weights(pkg, Q4_0, rows, cols, mid=42)
+    x = acts(pkg, m, cols, mid=42)
+    xb = pkg.to_bf16_bits(x)
+    x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
+    d_w, d_x = up(torch, raw), up(torch, xb.view(np.int16))
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(Q4_0, d_w.data_ptr(), raw.size, d_x.data_ptr(), BF16, d_y.data_ptr(), m, rows, cols,
+              stream(torch))
+    d_xf = up(torch, x_fed[m - 1])
+    d_g = torch.empty(rows, dtype=torch.float32, device="cuda")
+    pkg.qgemv(Q4_0, d_w.data_ptr(), raw.size, d_xf.data_ptr(), d_g.data_ptr(), rows, cols,
+              stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.all(np.isfinite(y))
+    g = down(d_g)
+    # both paths are within the contract of the same exact product, so they
+    # agree to twice the normalized tolerance
+    deq = orc.dequantize(Q4_0, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(y[m - 1], g, deq, x_fed[m - 1]) <= 2 * TOL
+
+
+# ------------------------------------------------------ activation quantizer
+
+@pytest.mark.parametrize("x_type", [F32, BF16])
+def test_quantize_q8_0_matches_host(pkg, torch_dev, x_type):
+    torch = torch_dev
+    n = 4096 * 33
+    x = acts(pkg, 1, n, mid=8)[0]
+    if x_type == BF16:
+        xb = pkg.to_bf16_bits(x)
+        x = (xb.astype(np.uint32) << 16).view(np.float32)
+        d_x = up(torch, xb.view(np.int16))
+    else:
+        d_x = up(torch, x)
+    d_q = torch.empty(n // 32 * 34, dtype=torch.uint8, device="cuda")
+    pkg.quantize_q8_0(d_x.data_ptr(), x_type, d_q.data_ptr(), n, stream(torch))
+    torch.cuda.synchronize()
+    host = pkg.quantize(Q8_0, x.reshape(1, -1))
+    assert np.array_equal(down(d_q), host)
+
+
+# ------------------------------------------------------------ legacy exports
+
+def test_legacy_fused_gemv_q4k_host_pointers(pkg, orc, torch_dev):
+    rows, cols = 333, 2048
+    raw = weights(pkg, Q4_K, rows, cols, mid=11)
+    x = acts(pkg, 1, cols, mid=11)[0]
+    out = np.full(rows, 5.0, np.float32)
+    pkg.gpu_lib().swamp_fused_gemv_q4k(raw.ctypes.data, x.ctypes.data, out.ctypes.data, rows, cols)
+    ref = orc.fused_gemv_q4k(raw, x, rows, cols)
+    deq = orc.dequantize(Q4_K, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(out, ref, deq, x) <= TOL
+
+
+def test_legacy_gemv_q8_vnni_kat(pkg, orc, fixtures, torch_dev):
+    L = pkg.gpu_lib()
+    for t in fixtures["int8_dot_kat"]:
+        w = np.array(t["w"], dtype=np.int8)
+        a = np.array(t["a"], dtype=np.int8)
+        got = L.swamp_gemv_q8_vnni(w.ctypes.data, a.ctypes.data, t["k"], 1.0)
+        assert got == float(np.float32(t["dot"]))
+        assert L.swamp_gemv_q8_vnni(w.ctypes.data, a.ctypes.data, t["k"], 0.5) == \
+            orc.gemv_q8_dot(w, a, 0.5)

@@ -1,0 +1,289 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline workload (one "step"): the Llama-3-8B decode layer sweep in Q4_0 at
+batch 1 -- five GEMVs y = W x, fp32 x ~ N(0,1), W ~ N(0,0.02) quantized to
+Q4_0 on the host:
+    fused QKV 6144x4096, O-proj 4096x4096, fused gate+up 28672x4096,
+    down 4096x14336, lm_head 128256x4096.
+value = algorithmic bytes of one step / wall time of one step (GB/s), with
+the weights already resident in HBM.  Algorithmic bytes per matrix =
+rows*K*18/32 (Q4_0 blocks) + K*4 (x) + rows*4 (y).
+
+Several full copies of the weight set (> 2x the 256 MB Infinity Cache in
+total) are rotated step by step so every weight byte comes from HBM.
+
+Also reported (outside the timed steps):
+  * roofline of the dominant kernel (the Q4_0 GEMV on lm_head, 70% of the
+    step's bytes): its algorithmic bytes / its mean launch duration, timed
+    with HIP events recorded on the launch stream around each of its
+    launches inside the timed region;
+  * per-matrix GB/s (each matrix timed alone, outside the timed region);
+  * the Q4_0 prefill GEMM at 2048 tokens (bf16 activations, matrix cores):
+    TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 peak;
+  * cpu_baseline: the reference's CPU matmul path (forward_linear fallback:
+    dequantize the whole tensor on one thread, then a row-partitioned f32
+    dot), restated in C, timed on this host's cores on one step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--no-prefill] [--cpu-threads T]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+
+DECODE_SHAPES = [              # (name, rows, K), Llama-3-8B, Q4_0
+    ("qkv", 6144, 4096),
+    ("o_proj", 4096, 4096),
+    ("gate_up", 28672, 4096),
+    ("down", 4096, 14336),
+    ("lm_head", 128256, 4096),
+]
+PREFILL_SHAPES = [("gate_up", 28672, 4096), ("down", 4096, 14336), ("qkv", 6144, 4096)]
+PREFILL_M = 2048
+SEED = 0x5EED
+
+
+def _load(name, path):
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def alg_bytes_gemv(dtype_bytes_per_32, rows, k, n_tok=1):
+    return rows * k * dtype_bytes_per_32 // 32 + n_tok * k * 4 + n_tok * rows * 4
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the GEMV kernel, from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel
+    calibration); None when no such summary exists."""
+    path = os.path.join(REPO, "profiles", "gemv_q4_0_llama3_8b_decode_traffic.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def cpu_baseline(pkg, n_threads, min_seconds=10.0):
+    """The reference's CPU path (oracle restatement of forward_linear's
+    dequantize-then-dot fallback, swamp-engine/src/linear.rs:68-88) on one
+    full decode step; returns GB/s over the same algorithmic bytes."""
+    orc = _load("swamp_oracle_py", os.path.join(REPO, "oracle", "oracle.py"))
+    mats = []
+    for i, (_, rows, k) in enumerate(DECODE_SHAPES):
+        raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ i, 0.02, rows, k)
+        x = pkg.fill_normal(SEED ^ 0xA11CE ^ i, 1.0, 1, k)[0]
+        mats.append((raw, x, rows, k))
+    total = sum(alg_bytes_gemv(18, r, k) for _, _, r, k in mats)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - t_start < min_seconds:
+        t0 = time.perf_counter()
+        for raw, x, rows, k in mats:
+            orc.forward_linear(pkg.Q4_0, raw, x, rows, k, n_threads)
+        times.append(time.perf_counter() - t0)
+    t = float(sum(times) / len(times))
+    return {
+        "value": round(total / t / 1e9, 4),
+        "unit": "GB/s",
+        "cores": n_threads,
+        "kind": "port",
+        "sample": (f"full decode steps (5 Q4_0 GEMVs, {total} algorithmic bytes each), mean of "
+                   f"{len(times)} reps ({sum(times):.1f} s), {n_threads} threads "
+                   f"({os.cpu_count()} visible); "
+                   "C restatement of forward_linear's fallback: allocate rows*K f32, "
+                   "dequantize on one thread, row-partitioned sequential f32 dot"),
+        "seconds_per_step": round(t, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=6,
+                    help="threads of the CPU baseline (the reference's pool size is 6)")
+    ap.add_argument("--copies", type=int, default=3, help="weight-set copies rotated per step")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path has no "
+              "multi-GPU code: row-sharding across GPUs is a design note, not a build.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    pkg = _load("llamanyon_rs_amd", os.path.join(REPO, "llamanyon.rs_amd", "__init__.py"))
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    torch.cuda.set_device(0)
+    pkg.init()
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+
+    # ---- data: one host-quantized weight set, cloned on the device -------
+    sets = [[] for _ in range(args.copies)]
+    xs, ys = [], []
+    for i, (_, rows, k) in enumerate(DECODE_SHAPES):
+        raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ i, 0.02, rows, k)
+        d0 = torch.from_numpy(raw).cuda()
+        sets[0].append(d0)
+        for c in range(1, args.copies):
+            sets[c].append(d0.clone())
+        xs.append(torch.from_numpy(pkg.fill_normal(SEED ^ 0xA11CE ^ i, 1.0, 1, k)[0]).cuda())
+        ys.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
+    step_bytes = sum(alg_bytes_gemv(18, r, k) for _, r, k in DECODE_SHAPES)
+    rotated = sum(t.numel() for st in sets for t in st)
+    lib = pkg.gpu_lib()
+
+    def launch(c, i):
+        _, rows, k = DECODE_SHAPES[i]
+        w = sets[c][i]
+        rc = lib.swamp_qgemv(pkg.Q4_0, w.data_ptr(), w.numel(), xs[i].data_ptr(),
+                             ys[i].data_ptr(), rows, k, s)
+        if rc != 0:
+            raise pkg.GpuError(rc, "swamp_qgemv")
+
+    for it in range(args.warmup):
+        for i in range(len(DECODE_SHAPES)):
+            launch(it % args.copies, i)
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly K steps ------------------------------------
+    # HIP events (on the launch stream) bracket every launch of the dominant
+    # kernel -- the lm_head GEMV, 70% of the step's bytes -- and nothing
+    # else, so the step itself runs back to back.
+    n = len(DECODE_SHAPES)
+    dom = max(range(n), key=lambda i: DECODE_SHAPES[i][1] * DECODE_SHAPES[i][2])
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for it in range(args.steps):
+        for i in range(n):
+            if i == dom:
+                ev[it][0].record(stream)
+            launch(it % args.copies, i)
+            if i == dom:
+                ev[it][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    dom_name, dom_rows, dom_k = DECODE_SHAPES[dom]
+    dom_bytes = alg_bytes_gemv(18, dom_rows, dom_k)
+    dom_us = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e3
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    traffic = traffic_from_profiles()
+    roofline = {"bound": "hbm", "kernel": f"gemv_kernel<Q4_0> on {dom_name} "
+                                          f"{dom_rows}x{dom_k}",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic, "alg_bytes_per_launch": dom_bytes,
+                "avg_launch_us": round(dom_us, 2)}
+
+    # ---- per-matrix kernel times (outside the timed region) --------------
+    # Each matrix alone, 20 back-to-back launches over the rotated copies,
+    # queued behind a GPU sleep so the host never starves the GPU.
+    shapes = []
+    for i, (name, rows, k) in enumerate(DECODE_SHAPES):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        e0.record(stream)
+        for it in range(20):
+            launch(it % args.copies, i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 20
+        b = alg_bytes_gemv(18, rows, k)
+        shapes.append({"name": name, "rows": rows, "k": k, "bytes": b, "us": round(us, 2),
+                       "GB/s": round(b / (us * 1e-6) / 1e9, 1),
+                       "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+
+    # ---- prefill GEMM, 2048 tokens, bf16 activations ----------------------
+    prefill = None
+    if not args.no_prefill:
+        prefill = []
+        for i, (name, rows, k) in enumerate(PREFILL_SHAPES):
+            raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x100 ^ i, 0.02, rows, k)
+            w = torch.from_numpy(raw).cuda()
+            xb = pkg.to_bf16_bits(pkg.fill_normal(SEED ^ 0x200 ^ i, 1.0, PREFILL_M, k))
+            x = torch.from_numpy(xb.view(np.int16)).cuda()
+            y = torch.empty((PREFILL_M, rows), dtype=torch.float32, device="cuda")
+
+            def g():
+                rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), x.data_ptr(), pkg.BF16,
+                                     y.data_ptr(), PREFILL_M, rows, k, s)
+                if rc != 0:
+                    raise pkg.GpuError(rc, "swamp_qgemm")
+            for _ in range(3):
+                g()
+            reps = 10
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            tflops = 2.0 * PREFILL_M * rows * k / (us * 1e-6) / 1e12
+            prefill.append({"name": name, "m": PREFILL_M, "rows": rows, "k": k,
+                            "x": "bf16", "us": round(us, 1), "TFLOP/s": round(tflops, 1),
+                            "frac_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)})
+            del w, x, y
+
+    cpu = None if args.no_cpu else cpu_baseline(pkg, args.cpu_threads)
+
+    out = {
+        "metric": "decode Q4 GEMV HBM GB/s (% peak) at 8B shapes; prefill GEMM TOPS @2048 tok",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 x f16 -> f32",
+        "data": "synthetic (W ~ N(0,0.02) quantized to Q4_0 on the host, x ~ N(0,1) fp32)",
+        "config": {"workload": "llama3-8b decode layer sweep, Q4_0, batch 1: qkv 6144x4096, "
+                               "o_proj 4096x4096, gate_up 28672x4096, down 4096x14336, "
+                               "lm_head 128256x4096",
+                   "step_alg_bytes": step_bytes, "weight_copies_rotated": args.copies,
+                   "rotated_weight_bytes": rotated, "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "shapes": shapes,
+        "prefill": prefill,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

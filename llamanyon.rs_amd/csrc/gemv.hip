@@ -7,19 +7,32 @@
 // Design (HBM-bound; 0.5625 B/weight for Q4_0/Q4_K, 1.0625 for Q8_0):
 //  * A row is cut into 64-weight "items" (two Q4_0 blocks = 36 B, two Q8_0
 //    blocks = 68 B, a quarter Q4_K super-block = 32 B of nibbles + the 16 B
-//    header).  Lane j of a workgroup always owns item j of every row, so its
-//    64 x values are loaded ONCE into registers and reused for every row the
-//    workgroup visits (workgroups are persistent over row tiles).
-//  * Q4_0/Q4_K: x is held as bf16 pairs; nibbles become bf16 (128 + q) with
-//    one and-or per pair and are multiplied by V_DOT2_F32_BF16 (two MACs
-//    per instruction, fp32 accumulate).  The 128 (+8 for Q4_0) offset is
-//    removed per block with the block sum of the same bf16 x values.
-//  * Q8_0: fp32 x, int8 -> fp32 converts (byte-select converts), fp32 FMA.
-//  * Each lane's partials are summed over the wavefront, then over the
-//    waves of the workgroup through LDS, once per tile of kRows rows.
+//    header).  Lane j of a workgroup always owns item j (+ T, + 2T, ...) of
+//    every row, so its x values are loaded ONCE into registers and reused
+//    for every row the workgroup visits (workgroups are persistent over
+//    tiles of kRows rows).
+//  * Tiles are double-buffered in registers: the loads of the next tile are
+//    issued (unconditionally, so the wait counts stay exact) before the
+//    current tile is reduced, so a wave never waits on HBM latency between
+//    tiles.
+//  * Weights become fp16 pairs with one and-or each: a low nibble q under
+//    the magic 0x6400 is 1024 + q, a high nibble left in place is
+//    1024 + 16 q (its x is pre-divided by 16), an int8 byte flipped to
+//    q + 128 is 1024 + q + 128.  V_DOT2_F32_F16 multiplies a pair by two
+//    fp16 x values exactly and accumulates in fp32; the constant offset is
+//    removed per block with the matching weighted sum of the same fp16 x
+//    values.  Per 8 nibbles: 1 shift + 4 and-or + 4 dot2.
+//  * x is converted to fp16 per item after scaling by a power of two that
+//    puts the item's largest |x| in [2^14, 2^15) (exact; fp16 range safe);
+//    the item's result is scaled back.
+//  * The kRows partial sums of a lane are reduced over the wavefront with a
+//    transposed butterfly (cross-half exchanges first, each halving the
+//    number of live values, then DPP adds), then over the waves of the
+//    workgroup through LDS.
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace {
@@ -29,35 +42,39 @@ using swamp::load_raw;
 using swamp::q4k_scales;
 using swamp::shr16;
 
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
-
-constexpr uint32_t kBf16Magic = 0x43004300u;  // bf16 pair (128, 128)
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c,
-                                         false);
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c,
+                                false);
 }
 
-// f32 -> bf16 bits, round to nearest even (x is finite activations).
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u) return (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+// Two floats -> packed fp16 pair, round to nearest even (V_CVT_PK_F16_F32).
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+  half2_t v;
+  v[0] = (_Float16)lo;
+  v[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, v);
 }
-__device__ __forceinline__ float bf16_val(uint32_t b) { return __uint_as_float(b << 16); }
 
-// Four bf16 pairs of one nibble dword w: pairs of (byte0, byte2) and
-// (byte1, byte3) low nibbles, then the same for the high nibbles.
-//   P0 = nib(w, 0), nib(w, 16)     P1 = nib(w, 8),  nib(w, 24)
-//   P2 = nib(w, 4), nib(w, 20)     P3 = nib(w, 12), nib(w, 28)
-__device__ __forceinline__ float dot_nib_dword(uint32_t w, const uint32_t *xp, float acc) {
-  acc = dot2((w & 0x000F000Fu) | kBf16Magic, xp[0], acc);
-  acc = dot2(((w >> 8) & 0x000F000Fu) | kBf16Magic, xp[1], acc);
-  acc = dot2(((w >> 4) & 0x000F000Fu) | kBf16Magic, xp[2], acc);
-  acc = dot2(((w >> 12) & 0x000F000Fu) | kBf16Magic, xp[3], acc);
-  return acc;
+// fp16 pair (1024, 1024) in a VGPR the compiler cannot see through, so that
+// (w & mask) | magic selects V_AND_OR_B32 with the mask in an SGPR (gfx9
+// VOP3 encodings take no literal).
+__device__ __forceinline__ uint32_t f16_magic() {
+  uint32_t m;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
+
+// Four fp16 pairs of one nibble dword w:
+//   P0 = lo(b0), lo(b2)   P1 = lo(b1), lo(b3)     (value 1024 + q)
+//   P2 = hi(b0), hi(b2)   P3 = hi(b1), hi(b3)     (value 1024 + 16 q)
+__device__ __forceinline__ void nib_pairs(uint32_t w, uint32_t m, uint32_t (&P)[4]) {
+  const uint32_t s = w >> 8;
+  P[0] = (w & 0x000F000Fu) | m;
+  P[1] = (s & 0x000F000Fu) | m;
+  P[2] = (w & 0x00F000F0u) | m;
+  P[3] = (s & 0x00F000F0u) | m;
 }
 
 // Element (0..63 within the item) that half h of pair p of nibble dword t
@@ -66,119 +83,225 @@ __device__ __forceinline__ float dot_nib_dword(uint32_t w, const uint32_t *xp, f
 //         (interleaved layout, q4_0.rs:30-35), t' = t%4;
 //   Q4_K: low nibble of byte b -> sub-block A element 4t+b,
 //         high nibble -> sub-block B (item elements 32..63) element 4t+b.
+// Pairs p = 2, 3 hold high nibbles (their x is divided by 16).
 template <int DT>
 __host__ __device__ constexpr int nib_elem(int t, int p, int h) {
-  // bit offset of the nibble for (p, h)
-  // p0: 0,16  p1: 8,24  p2: 4,20  p3: 12,28
-  const int bit = (p == 0 ? 0 : p == 1 ? 8 : p == 2 ? 4 : 12) + 16 * h;
-  const int byte = bit / 8, high = (bit % 8) != 0;
+  const int byte = (p & 1) + 2 * h;  // P0: b0,b2  P1: b1,b3  P2: b0,b2  P3: b1,b3
+  const int high = p >= 2;
   if (DT == SWAMP_Q4_0) return 32 * (t / 4) + 8 * (t % 4) + 2 * byte + high;
   return 32 * high + 4 * t + byte;  // Q4_K
 }
 
-// Per-lane x fragment for one item.
+// Element of half h of pair j (0, 1) of int8 dword t of a Q8_0 item (after
+// the block-0 bytes are realigned): bytes j and j + 2.
+__host__ __device__ constexpr int q8_elem(int t, int j, int h) { return 4 * t + j + 2 * h; }
+
+// Per-lane x fragment for one item: fp16 pairs in the order the weight
+// pairs are formed, the offset corrections, and the item's scale 2^e.
 template <int DT>
 struct XFrag;
 
 template <>
 struct XFrag<SWAMP_Q4_0> {
-  uint32_t p[32];  // 8 nibble dwords x 4 bf16 pairs
-  float c[2];      // 136 * sum of the block's bf16 x (removes the +128 and -8)
+  uint32_t p[32];  // 8 nibble dwords x 4 pairs
+  float c[2];      // per block: sum of 1032 x (low) + 1152 x/16 (high)
+  float scale;
 };
 template <>
 struct XFrag<SWAMP_Q4_K> {
   uint32_t p[32];
-  float sa, sb;  // sum of bf16 x over sub-block A and B
+  float sa;    // sum of x over sub-block A (low nibbles)
+  float sb16;  // sum of x/16 over sub-block B (high nibbles)
+  float scale;
 };
 template <>
 struct XFrag<SWAMP_Q8_0> {
-  float v[64];
+  uint32_t p[32];  // 16 int8 dwords x 2 pairs
+  float c[2];      // per block: 1152 * sum of x
+  float scale;
 };
 
-template <int DT>
-__device__ __forceinline__ void load_xfrag(XFrag<DT> &xf, const float *__restrict__ x, int item) {
+// Issue the loads of one item's 64 x values (clamped item: always in
+// bounds; a lane past the row end zeroes its values afterwards).
+__device__ __forceinline__ void load_x(float4 (&xv)[16], const float *__restrict__ x, int item) {
   const float4 *xp = reinterpret_cast<const float4 *>(x + size_t(item) * 64);
+#pragma unroll
+  for (int i = 0; i < 16; i++) xv[i] = xp[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void build_xfrag(XFrag<DT> &xf, const float4 (&x4)[16], bool valid) {
   float xv[64];
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    float4 f = xp[i];
-    xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+    xv[4 * i] = x4[i].x; xv[4 * i + 1] = x4[i].y; xv[4 * i + 2] = x4[i].z; xv[4 * i + 3] = x4[i].w;
   }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; i++) {
+    xv[i] = valid ? xv[i] : 0.f;
+    amax = fmaxf(amax, fabsf(xv[i]));
+  }
+  // scale 2^(141 - E) maps amax (biased exponent E) into [2^14, 2^15)
+  int E = int((__float_as_uint(amax) >> 23) & 0xFFu);
+  E = E < 15 ? 15 : E > 254 ? 254 : E;
+  const float down = __uint_as_float(uint32_t(268 - E) << 23);
+  xf.scale = __uint_as_float(uint32_t(E - 14) << 23);
+  const float down16 = down * 0.0625f;
+  const uint32_t k_lo = 0x64086408u;  // fp16 pair (1032, 1032)
+  const uint32_t k_hi = 0x64806480u;  // fp16 pair (1152, 1152)
+  const uint32_t k_one = 0x3C003C00u;  // fp16 pair (1, 1)
   if constexpr (DT == SWAMP_Q8_0) {
+    float c0 = 0.f, c1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 64; i++) xf.v[i] = xv[i];
+    for (int t = 0; t < 16; t++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const uint32_t pr = pack_f16(xv[q8_elem(t, j, 0)] * down, xv[q8_elem(t, j, 1)] * down);
+        xf.p[2 * t + j] = pr;
+        if (t < 8) c0 = dot2(k_hi, pr, c0);
+        else c1 = dot2(k_hi, pr, c1);
+      }
+    xf.c[0] = c0;
+    xf.c[1] = c1;
   } else {
-    uint32_t xb[64];
-#pragma unroll
-    for (int i = 0; i < 64; i++) xb[i] = bf16_rne(xv[i]);
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++)
 #pragma unroll
-      for (int p = 0; p < 4; p++)
-        xf.p[4 * t + p] = xb[nib_elem<DT>(t, p, 0)] | (xb[nib_elem<DT>(t, p, 1)] << 16);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      s0 += bf16_val(xb[i]);
-      s1 += bf16_val(xb[32 + i]);
-    }
+      for (int p = 0; p < 4; p++) {
+        const float f = p >= 2 ? down16 : down;
+        const uint32_t pr = pack_f16(xv[nib_elem<DT>(t, p, 0)] * f, xv[nib_elem<DT>(t, p, 1)] * f);
+        xf.p[4 * t + p] = pr;
+        if constexpr (DT == SWAMP_Q4_0) {
+          // both halves of a pair lie in block t / 4
+          if (t < 4) s0 = dot2(p >= 2 ? k_hi : k_lo, pr, s0);
+          else s1 = dot2(p >= 2 ? k_hi : k_lo, pr, s1);
+        } else {
+          if (p < 2) s0 = dot2(k_one, pr, s0);
+          else s1 = dot2(k_one, pr, s1);
+        }
+      }
     if constexpr (DT == SWAMP_Q4_0) {
-      xf.c[0] = 136.0f * s0;
-      xf.c[1] = 136.0f * s1;
+      xf.c[0] = s0;
+      xf.c[1] = s1;
     } else {
       xf.sa = s0;
-      xf.sb = s1;
+      xf.sb16 = s1;
     }
   }
 }
 
 template <int DT>
-__device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf, int item) {
+__device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf, int item,
+                                          uint32_t m) {
   if constexpr (DT == SWAMP_Q4_0) {
     const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
     const float d1 = swamp::f16_bits_to_f32(r.d[4] >> 16);
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int t = 0; t < 4; t++) s0 = dot_nib_dword(shr16(r.d[t + 1], r.d[t]), &xf.p[4 * t], s0);
+    for (int t = 0; t < 8; t++) {
+      const uint32_t w = t < 4 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1];
+      uint32_t P[4];
+      nib_pairs(w, m, P);
 #pragma unroll
-    for (int t = 0; t < 4; t++) s1 = dot_nib_dword(r.d[5 + t], &xf.p[16 + 4 * t], s1);
-    return d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1]);
+      for (int p = 0; p < 4; p++) {
+        if (t < 4) s0 = dot2(P[p], xf.p[4 * t + p], s0);
+        else s1 = dot2(P[p], xf.p[4 * t + p], s1);
+      }
+    }
+    return (d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1])) * xf.scale;
   } else if constexpr (DT == SWAMP_Q8_0) {
     const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
     const float d1 = swamp::f16_bits_to_f32(r.d[8] >> 16);
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const uint32_t w = shr16(r.d[t + 1], r.d[t]);
-#pragma unroll
-      for (int b = 0; b < 4; b++) s0 += float(int8_t(uint8_t(w >> (8 * b)))) * xf.v[4 * t + b];
+    for (int t = 0; t < 16; t++) {
+      const uint32_t w = (t < 8 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1]) ^ 0x80808080u;
+      const uint32_t P0 = (w & 0x00FF00FFu) | m;
+      const uint32_t P1 = ((w >> 8) & 0x00FF00FFu) | m;
+      if (t < 8) {
+        s0 = dot2(P0, xf.p[2 * t], s0);
+        s0 = dot2(P1, xf.p[2 * t + 1], s0);
+      } else {
+        s1 = dot2(P0, xf.p[2 * t], s1);
+        s1 = dot2(P1, xf.p[2 * t + 1], s1);
+      }
     }
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const uint32_t w = r.d[9 + t];
-#pragma unroll
-      for (int b = 0; b < 4; b++) s1 += float(int8_t(uint8_t(w >> (8 * b)))) * xf.v[32 + 4 * t + b];
-    }
-    return d0 * s0 + d1 * s1;
+    return (d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1])) * xf.scale;
   } else {
     const float d = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
     q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
-    // low nibbles -> sub-block A, high -> B; pairs P0,P1 are low, P2,P3 high
     float sa = 0.f, sb = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-      const uint32_t w = r.q[t];
-      sa = dot2((w & 0x000F000Fu) | kBf16Magic, xf.p[4 * t + 0], sa);
-      sa = dot2(((w >> 8) & 0x000F000Fu) | kBf16Magic, xf.p[4 * t + 1], sa);
-      sb = dot2(((w >> 4) & 0x000F000Fu) | kBf16Magic, xf.p[4 * t + 2], sb);
-      sb = dot2(((w >> 12) & 0x000F000Fu) | kBf16Magic, xf.p[4 * t + 3], sb);
+      uint32_t P[4];
+      nib_pairs(r.q[t], m, P);
+      sa = dot2(P[0], xf.p[4 * t + 0], sa);
+      sa = dot2(P[1], xf.p[4 * t + 1], sa);
+      sb = dot2(P[2], xf.p[4 * t + 2], sb);
+      sb = dot2(P[3], xf.p[4 * t + 3], sb);
     }
-    // sum (d*sc*q - dmin*m) x = d*sc*(S - 128 Sx) - dmin*m*Sx
-    const float qa = sa - 128.0f * xf.sa, qb = sb - 128.0f * xf.sb;
-    return d * (float(sc0) * qa + float(sc1) * qb) - dmin * (float(m0) * xf.sa + float(m1) * xf.sb);
+    // sum (d*sc*q - dmin*m) x = d*sc*(S - 1024 Sx) - dmin*m*Sx, with B's x
+    // carried as x/16
+    const float qa = sa - 1024.0f * xf.sa, qb = sb - 1024.0f * xf.sb16;
+    return (d * (float(sc0) * qa + float(sc1) * qb) -
+            dmin * (float(m0) * xf.sa + float(m1) * 16.0f * xf.sb16)) *
+           xf.scale;
   }
+}
+
+// ---- wavefront reduction of kRows partial sums ---------------------------
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+
+// One transposed butterfly level on lane bit `off`: lanes with the bit clear
+// keep values [0, n/2), lanes with it set keep [n/2, n); each lane adds the
+// partner's copy of the values it keeps.
+template <int N>
+__device__ __forceinline__ void tr_level(float (&v)[N], int n, int off, int lane) {
+  const bool up = (lane & off) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; i++) {
+    if (i < n / 2) {
+      const float send = up ? v[i] : v[i + n / 2];
+      const float keep = up ? v[i + n / 2] : v[i];
+      v[i] = keep + __shfl_xor(send, off, 64);
+    }
+  }
+}
+
+// After reduce_rows<R>, lane l holds the wavefront total of row
+// l >> (6 - log2 R) in v[0].  The xor masks used (32, 16, 15 = row mirror,
+// 7 = half-row mirror, 2, 1) are linearly independent over GF(2), so every
+// lane's partial is counted exactly once; masks after a transposed level
+// never flip that level's bit.
+template <int R>
+__device__ __forceinline__ void reduce_rows(float (&v)[R], int lane) {
+  static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per tile");
+  if constexpr (R >= 2) tr_level<R>(v, R, 32, lane);
+  else v[0] += __shfl_xor(v[0], 32, 64);
+  if constexpr (R >= 4) tr_level<R>(v, R / 2, 16, lane);
+  else v[0] += __shfl_xor(v[0], 16, 64);
+  if constexpr (R >= 8) {
+    // bit 3 through the row mirror (lane ^ 15): its bits 0..2 flips are
+    // harmless because the later levels reduce over those bits anyway.
+    const bool up = (lane & 8) != 0;
+    const float send = up ? v[0] : v[1];
+    const float keep = up ? v[1] : v[0];
+    v[0] = keep + dpp<0x140>(send);
+  } else {
+    v[0] += dpp<0x140>(v[0]);  // row mirror
+  }
+  v[0] += dpp<0x141>(v[0]);  // half-row mirror (lane ^ 7)
+  v[0] += dpp<0x4E>(v[0]);   // quad_perm [2,3,0,1]
+  v[0] += dpp<0xB1>(v[0]);   // quad_perm [1,0,3,2]
 }
 
 constexpr int kMaxMats = SWAMP_MULTI_MAX;
@@ -191,74 +314,132 @@ struct MatSet {
   int n;
 };
 
-// One workgroup = 64 * nwaves lanes; lane j owns items j, j + T, ...
-// (kPPT items per lane), covering one row of ipr items.  The workgroup
-// loops over row tiles of kRows rows.
-template <int DT, int kPPT, int kRows>
-__global__ void __launch_bounds__(512) gemv_kernel(MatSet ms, const float *__restrict__ x,
-                                                   int ipr, size_t row_bytes, int n_tiles) {
-  __shared__ float red[2][8][kRows];
-  const int tid = threadIdx.x;
-  const int T = blockDim.x;
-  const int nw = T >> 6, wave = tid >> 6, lane = tid & 63;
+struct TileRef {
+  const uint8_t *w;
+  float *y;
+  int row0, nrows;
+};
 
-  XFrag<DT> xf[kPPT];
+template <int kRows, bool kMulti>
+__device__ __forceinline__ TileRef tile_ref(const MatSet &ms, int tile) {
+  if constexpr (!kMulti) return TileRef{ms.w[0], ms.y[0], tile * kRows, ms.rows[0]};
+  int m = 0;
+  while (m + 1 < ms.n && tile >= ms.tile_end[m]) m++;
+  const int first = m ? ms.tile_end[m - 1] : 0;
+  return TileRef{ms.w[m], ms.y[m], (tile - first) * kRows, ms.rows[m]};
+}
+
+// One buffer descriptor per tile (base = the tile's first row); row r of
+// the tile is the scalar offset r * row_bytes (rows past the matrix end
+// are clamped to its last row, so every load stays in bounds).
+template <int DT, int kPPT, int kRows>
+__device__ __forceinline__ void issue_tile(Raw<DT> (&raw)[kRows][kPPT], const TileRef &t,
+                                           size_t row_bytes, const int (&item)[kPPT],
+                                           const uint32_t (&off)[kPPT]) {
+  const uint32_t rb = uint32_t(row_bytes);
+  const __amdgpu_buffer_rsrc_t rs =
+      swamp::make_rsrc(t.w + size_t(t.row0) * row_bytes, rb * kRows);
+#pragma unroll
+  for (int r = 0; r < kRows; r++) {
+    const int rr = min(t.row0 + r, t.nrows - 1) - t.row0;
+#pragma unroll
+    for (int j = 0; j < kPPT; j++)
+      swamp::load_raw_buf<DT>(raw[r][j], rs, off[j], uint32_t(rr) * rb, item[j]);
+  }
+}
+
+template <int DT, int kPPT, int kRows, int kWaves>
+__device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
+                                             const XFrag<DT> (&xf)[kPPT], const TileRef &t,
+                                             const int (&item)[kPPT],
+                                             float (*red)[kRows], int tid, uint32_t m) {
+  const int lane = tid & 63, wave = tid >> 6;
+  float acc[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; r++) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPPT; j++) acc[r] += item_dot<DT>(raw[r][j], xf[j], item[j], m);
+  }
+  reduce_rows<kRows>(acc, lane);
+  constexpr int kGroup = 64 / kRows;  // lanes holding one row's total
+  const int rr = lane / kGroup;
+  if constexpr (kWaves == 1) {
+    if (lane % kGroup == 0 && t.row0 + rr < t.nrows) t.y[t.row0 + rr] = acc[0];
+  } else {
+    if (lane % kGroup == 0) red[wave][rr] = acc[0];
+    __syncthreads();
+    if (tid < kRows && t.row0 + tid < t.nrows) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; w++) v += red[w][tid];
+      t.y[t.row0 + tid] = v;
+    }
+  }
+}
+
+// One workgroup = 64 * kWaves lanes; lane j owns items j, j + T, ...
+// (kPPT items per lane), covering one row of ipr items.  The workgroup
+// walks tiles blockIdx.x, + gridDim.x, ... of kRows rows each.
+template <int DT, int kPPT, int kRows, int kWaves, bool kMulti>
+__global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const float *__restrict__ x,
+                                                           int ipr, size_t row_bytes,
+                                                           int n_tiles) {
+  constexpr int T = 64 * kWaves;
+  __shared__ float red[2][kWaves][kRows];
+  const int tid = threadIdx.x;
+
+  int item[kPPT];
   bool valid[kPPT];
 #pragma unroll
   for (int j = 0; j < kPPT; j++) {
-    const int item = tid + j * T;
-    valid[j] = item < ipr;
-    if (valid[j]) load_xfrag<DT>(xf[j], x, item);
+    const int it = tid + j * T;
+    valid[j] = it < ipr;
+    item[j] = valid[j] ? it : ipr - 1;  // in-bounds stand-in; its x is zero
   }
+  uint32_t off[kPPT];
+#pragma unroll
+  for (int j = 0; j < kPPT; j++) off[j] = swamp::item_offset<DT>(item[j]);
 
-  int par = 0;
-  for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x, par ^= 1) {
-    int m = 0;
-    while (m + 1 < ms.n && tile >= ms.tile_end[m]) m++;
-    const int first = m ? ms.tile_end[m - 1] : 0;
-    const int row0 = (tile - first) * kRows;
-    const int nrows = ms.rows[m];
-    const uint8_t *wbase = ms.w[m];
+  int tile = blockIdx.x;
+  if (tile >= n_tiles) return;
+  const uint32_t m = f16_magic();
 
-    float acc[kRows];
-    Raw<DT> raw[kRows][kPPT];
+  // x loads first, then the first tile's weight loads, then the x
+  // conversion (which waits for the x loads only).
+  float4 x4[kPPT][16];
 #pragma unroll
-    for (int r = 0; r < kRows; r++) {
-      acc[r] = 0.f;
-      const int row = row0 + r < nrows ? row0 + r : nrows - 1;  // clamp: stays in bounds
+  for (int j = 0; j < kPPT; j++) load_x(x4[j], x, item[j]);
+  Raw<DT> ra[kRows][kPPT], rb[kRows][kPPT];
+  TileRef ta = tile_ref<kRows, kMulti>(ms, tile);
+  issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
+  // keep every load of the tile ahead of the arithmetic (the scheduler would
+  // otherwise sink them into registers freed by the current tile)
+  __builtin_amdgcn_sched_barrier(0);
+  XFrag<DT> xf[kPPT];
 #pragma unroll
-      for (int j = 0; j < kPPT; j++)
-        if (valid[j]) load_raw<DT>(raw[r][j], wbase + size_t(row) * row_bytes, tid + j * T);
-    }
-#pragma unroll
-    for (int r = 0; r < kRows; r++)
-#pragma unroll
-      for (int j = 0; j < kPPT; j++)
-        if (valid[j]) acc[r] += item_dot<DT>(raw[r][j], xf[j], tid + j * T);
+  for (int j = 0; j < kPPT; j++) build_xfrag<DT>(xf[j], x4[j], valid[j]);
 
-#pragma unroll
-    for (int r = 0; r < kRows; r++) acc[r] = swamp::wave_sum(acc[r]);
-
-    float *y = ms.y[m];
-    if (nw == 1) {
-      if (lane < kRows && row0 + lane < nrows) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < kRows; r++) v = lane == r ? acc[r] : v;
-        y[row0 + lane] = v;
-      }
-    } else {
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < kRows; r++) red[par][wave][r] = acc[r];
-      }
-      __syncthreads();
-      if (tid < kRows && row0 + tid < nrows) {
-        float v = 0.f;
-        for (int w = 0; w < nw; w++) v += red[par][w][tid];
-        y[row0 + tid] = v;
-      }
-    }
+  // Two tiles per trip so both register buffers have static names.  The
+  // next tile's loads are issued unconditionally (past the last tile they
+  // re-read the current one, already in cache), so every path through the
+  // loop has the same number of loads in flight and the hardware wait
+  // counts stay tight.
+  for (;;) {
+    int nxt = tile + gridDim.x;
+    const TileRef tb = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
+    issue_tile<DT, kPPT, kRows>(rb, tb, row_bytes, item, off);
+    __builtin_amdgcn_sched_barrier(0);
+    consume_tile<DT, kPPT, kRows, kWaves>(ra, xf, ta, item, red[0], tid, m);
+    if (nxt >= n_tiles) break;
+    tile = nxt;
+    nxt = tile + gridDim.x;
+    ta = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
+    issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
+    __builtin_amdgcn_sched_barrier(0);
+    consume_tile<DT, kPPT, kRows, kWaves>(rb, xf, tb, item, red[1], tid, m);
+    if (nxt >= n_tiles) break;
+    tile = nxt;
   }
 }
 
@@ -299,12 +480,19 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(const uint8_t *__rest
   }
 }
 
+// Launch shape: waves per CU the persistent grid aims for, and rows per
+// tile (SWAMP_GEMV_WAVES_PER_CU / SWAMP_GEMV_ROWS override them).
 struct Tuning {
-  int waves_per_cu = 16;
+  int waves_per_cu = 4;
+  int rows = 0;  // 0: chosen per shape
   Tuning() {
     if (const char *s = std::getenv("SWAMP_GEMV_WAVES_PER_CU")) {
       int v = std::atoi(s);
       if (v >= 1 && v <= 64) waves_per_cu = v;
+    }
+    if (const char *s = std::getenv("SWAMP_GEMV_ROWS")) {
+      int v = std::atoi(s);
+      if (v == 1 || v == 2 || v == 4) rows = v;
     }
   }
 };
@@ -313,28 +501,22 @@ const Tuning &tuning() {
   return t;
 }
 
-template <int DT, int kPPT, int kRows>
+template <int DT, int kPPT, int kRows, int kWaves>
 int launch_items(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
   const int ipr = n_cols / 64;
-  int T = ((ipr + kPPT - 1) / kPPT + 63) / 64 * 64;
-  if (T > 512) return SWAMP_ESHAPE;
-  const int nw = T / 64;
+  if (ipr > kPPT * 64 * kWaves) return SWAMP_ESHAPE;
   const int n_tiles = ms.tile_end[ms.n - 1];
   const int cus = swamp::device_info().num_cus;
-  int grid = cus * std::max(1, tuning().waves_per_cu / nw);
+  int grid = cus * std::max(1, tuning().waves_per_cu / kWaves);
   if (grid > n_tiles) grid = n_tiles;
   if (grid < 1) return SWAMP_OK;
-  gemv_kernel<DT, kPPT, kRows><<<grid, T, 0, s>>>(ms, x, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
+  if (ms.n == 1)
+    gemv_kernel<DT, kPPT, kRows, kWaves, false>
+        <<<grid, 64 * kWaves, 0, s>>>(ms, x, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
+  else
+    gemv_kernel<DT, kPPT, kRows, kWaves, true>
+        <<<grid, 64 * kWaves, 0, s>>>(ms, x, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
-}
-
-template <int DT>
-int launch_dt(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
-  const int ipr = n_cols / 64;
-  if (ipr <= 512) return launch_items<DT, 1, 4>(ms, x, n_cols, s);
-  if (ipr <= 1024) return launch_items<DT, 2, 4>(ms, x, n_cols, s);
-  if (ipr <= 2048) return launch_items<DT, 4, 2>(ms, x, n_cols, s);
-  return SWAMP_ESHAPE;
 }
 
 int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, const int *rows,
@@ -351,16 +533,52 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
   return acc;
 }
 
-int dispatch(uint32_t dt, const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
-  switch (dt) {
-  case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0>(ms, x, n_cols, s);
-  case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0>(ms, x, n_cols, s);
-  case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K>(ms, x, n_cols, s);
-  default: return SWAMP_EDTYPE;
+// Waves per workgroup for a row of ipr items (matches launch_rows).
+int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
+
+// Rows per tile: 4 when every workgroup of the grid gets at least 8 tiles,
+// else 2 when it gets at least 2, else 1.  Longer tile runs per wave hide
+// the first tile's latency and the x prologue; shorter tiles keep small
+// matrices spread over the whole chip.
+int tile_rows_for(int n_cols, int total_rows) {
+  if (tuning().rows) return tuning().rows;
+  const int cus = swamp::device_info().num_cus;
+  const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(n_cols / 64));
+  if (long(total_rows) / 4 >= 8 * slots) return 4;
+  if (long(total_rows) / 2 >= 2 * slots) return 2;
+  return 1;
+}
+
+template <int DT, int kRows>
+int launch_rows(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
+  const int ipr = n_cols / 64;
+  if (ipr <= 64) return launch_items<DT, 1, kRows, 1>(ms, x, n_cols, s);
+  if (ipr <= 128) return launch_items<DT, 1, kRows, 2>(ms, x, n_cols, s);
+  if (ipr <= 256) return launch_items<DT, 1, kRows, 4>(ms, x, n_cols, s);
+  if (ipr <= 512) return launch_items<DT, 1, kRows, 8>(ms, x, n_cols, s);
+  if (ipr <= 1024) return launch_items<DT, 2, kRows, 8>(ms, x, n_cols, s);
+  if (ipr <= 2048) return launch_items<DT, 4, kRows, 8>(ms, x, n_cols, s);
+  return SWAMP_ESHAPE;
+}
+
+template <int DT>
+int launch_dt(const MatSet &ms, const float *x, int n_cols, int tile_rows, hipStream_t s) {
+  switch (tile_rows) {
+  case 4: return launch_rows<DT, 4>(ms, x, n_cols, s);
+  case 2: return launch_rows<DT, 2>(ms, x, n_cols, s);
+  default: return launch_rows<DT, 1>(ms, x, n_cols, s);
   }
 }
 
-int tile_rows_for(int n_cols) { return n_cols / 64 <= 1024 ? 4 : 2; }
+int dispatch(uint32_t dt, const MatSet &ms, const float *x, int n_cols, int tile_rows,
+             hipStream_t s) {
+  switch (dt) {
+  case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0>(ms, x, n_cols, tile_rows, s);
+  case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0>(ms, x, n_cols, tile_rows, s);
+  case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K>(ms, x, n_cols, tile_rows, s);
+  default: return SWAMP_EDTYPE;
+  }
+}
 
 }  // namespace
 
@@ -383,8 +601,9 @@ int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *
   MatSet ms;
   const void *ws[1] = {d_w};
   float *ys[1] = {d_y};
-  build_matset(ms, 1, ws, ys, &n_rows, tile_rows_for(n_cols));
-  return dispatch(dtype, ms, d_x, n_cols, s);
+  const int tr = tile_rows_for(n_cols, n_rows);
+  build_matset(ms, 1, ws, ys, &n_rows, tr);
+  return dispatch(dtype, ms, d_x, n_cols, tr, s);
 }
 
 int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
@@ -409,12 +628,13 @@ int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *cons
     const void *ws[kMaxMats];
     float *ys[kMaxMats];
     int rows[kMaxMats];
-    int n = 0;
+    int n = 0, total = 0;
     for (int j = i; j < n_mats; j++)
       if (!done[j] && dtypes[j] == dt && row_counts[j] > 0) {
         ws[n] = d_ws[j];
         ys[n] = d_ys[j];
         rows[n] = row_counts[j];
+        total += row_counts[j];
         n++;
         done[j] = true;
       } else if (dtypes[j] == dt) {
@@ -422,8 +642,9 @@ int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *cons
       }
     if (n == 0) continue;
     MatSet ms;
-    build_matset(ms, n, ws, ys, rows, tile_rows_for(n_cols));
-    int rc = dispatch(dt, ms, d_x, n_cols, s);
+    const int tr = tile_rows_for(n_cols, total);
+    build_matset(ms, n, ws, ys, rows, tr);
+    int rc = dispatch(dt, ms, d_x, n_cols, tr, s);
     if (rc) return rc;
   }
   return SWAMP_OK;

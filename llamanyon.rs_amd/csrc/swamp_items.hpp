@@ -28,16 +28,27 @@ struct Raw<SWAMP_Q4_K> {
   uint32_t q[8];  // 32 nibble bytes of the quarter
 };
 
+// Byte offset of item `item` within its row (32-bit: rows are < 4 GiB), so
+// that loads take the uniform row pointer as a scalar base plus this
+// per-lane offset (global_load ... saddr), keeping no 64-bit address VGPRs.
 template <int DT>
-__device__ __forceinline__ void load_raw(Raw<DT> &r, const uint8_t *row, int item) {
+__device__ __forceinline__ uint32_t item_offset(int item) {
+  if constexpr (DT == SWAMP_Q4_0) return uint32_t(item) * 36u;
+  else if constexpr (DT == SWAMP_Q8_0) return uint32_t(item) * 68u;
+  else return uint32_t(item >> 2) * 144u + 16u + 32u * uint32_t(item & 3);
+}
+
+// Raw bytes of the item at byte offset `off` of `row` (from item_offset).
+template <int DT>
+__device__ __forceinline__ void load_raw_at(Raw<DT> &r, const uint8_t *row, uint32_t off, int item) {
   if constexpr (DT == SWAMP_Q4_0) {
-    const uint8_t *p = row + size_t(item) * 36;
+    const uint8_t *p = row + off;
     u32x4 a = ld4(p), b = ld4(p + 16);
 #pragma unroll
     for (int i = 0; i < 4; i++) { r.d[i] = a.v[i]; r.d[4 + i] = b.v[i]; }
     r.d[8] = ld1(p + 32);
   } else if constexpr (DT == SWAMP_Q8_0) {
-    const uint8_t *p = row + size_t(item) * 68;
+    const uint8_t *p = row + off;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       u32x4 a = ld4(p + 16 * j);
@@ -46,8 +57,8 @@ __device__ __forceinline__ void load_raw(Raw<DT> &r, const uint8_t *row, int ite
     }
     r.d[16] = ld1(p + 64);
   } else {
-    const uint8_t *blk = row + size_t(item >> 2) * 144;
-    const uint8_t *qs = blk + 16 + 32 * (item & 3);
+    const uint8_t *qs = row + off;
+    const uint8_t *blk = row + (off - 16u - 32u * uint32_t(item & 3));
     uint4 h = *reinterpret_cast<const uint4 *>(blk);
     uint4 a = *reinterpret_cast<const uint4 *>(qs);
     uint4 b = *reinterpret_cast<const uint4 *>(qs + 16);
@@ -55,6 +66,49 @@ __device__ __forceinline__ void load_raw(Raw<DT> &r, const uint8_t *row, int ite
     r.q[0] = a.x; r.q[1] = a.y; r.q[2] = a.z; r.q[3] = a.w;
     r.q[4] = b.x; r.q[5] = b.y; r.q[6] = b.z; r.q[7] = b.w;
   }
+}
+
+// Buffer resource over [base, base + bytes): raw (untyped) dword loads,
+// 32-bit data format (the gfx9 word-3 value), out-of-range reads return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, int(bytes), 0x00020000);
+}
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Raw bytes of one item through a buffer resource: the per-lane item offset
+// in a VGPR (voff) and the per-row offset in an SGPR (soff), so one row
+// pointer per tile (in the descriptor) serves every load of the tile.
+template <int DT>
+__device__ __forceinline__ void load_raw_buf(Raw<DT> &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                             uint32_t soff, int item) {
+  if constexpr (DT == SWAMP_Q4_0) {
+    const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16, soff, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) { r.d[i] = a[i]; r.d[4 + i] = b[i]; }
+    r.d[8] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 32, soff, 0);
+  } else if constexpr (DT == SWAMP_Q8_0) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * j, soff, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) r.d[4 * j + i] = a[i];
+    }
+    r.d[16] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 64, soff, 0);
+  } else {
+    const uint32_t hoff = voff - 16u - 32u * uint32_t(item & 3);
+    const u32x4v h = __builtin_amdgcn_raw_buffer_load_b128(rs, hoff, soff, 0);
+    const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16, soff, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) { r.h[i] = h[i]; r.q[i] = a[i]; r.q[4 + i] = b[i]; }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void load_raw(Raw<DT> &r, const uint8_t *row, int item) {
+  load_raw_at<DT>(r, row, item_offset<DT>(item), item);
 }
 
 __device__ __forceinline__ uint32_t shr16(uint32_t hi, uint32_t lo) {

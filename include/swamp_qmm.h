@@ -110,9 +110,13 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *   x_type SWAMP_BF16: d_x is bf16 [m][n_cols]; W is dequantized into LDS
  *     as bf16 and fed to bf16 MFMA (fp32 accumulate).
  *   x_type SWAMP_Q8_0: d_x is Q8_0 blocks [m][n_cols/32] (as produced by
- *     swamp_quantize_q8_0); int8 MFMA against W's int8 codes, fp32
- *     per-block rescale.  Q4_0 and Q8_0 weights only.
- * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only).  No workspace. */
+ *     swamp_quantize_q8_0); int8 MFMA (one 32x32x32 instruction per
+ *     32-weight block) against W's int8 codes (Q4_0: nibble - 8), each
+ *     block's int32 result scaled by d_w * d_x into fp32.  Q4_0 and Q8_0
+ *     weights only; n_cols a multiple of 128.
+ * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only); bf16 x needs n_cols a
+ * multiple of 64.  No workspace: when the tiles do not fill the GPU, K is
+ * split across workgroups that add into y (zeroed by a fill kernel first). */
 int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);

@@ -213,7 +213,7 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (x_type == SWAMP_Q8_0 && dtype == SWAMP_Q4_K) return SWAMP_EDTYPE;
   if (m == 0 || n_rows == 0) return SWAMP_OK;
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
-  if (n_cols % 64 != 0) return SWAMP_ESHAPE;
+  if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;
   if (int rc = ensure_device(nullptr)) return rc;
   return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols,
                            static_cast<hipStream_t>(stream));

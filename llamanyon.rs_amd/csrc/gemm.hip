@@ -403,7 +403,8 @@ int set_smem_attr() {
 int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t x_type,
                       float *d_y, int m, int n_rows, int n_cols, hipStream_t s) {
   if (m == 0 || n_rows == 0) return SWAMP_OK;
-  if (x_type != SWAMP_BF16) return SWAMP_EDTYPE;  // int8 path: not built yet
+  if (x_type == SWAMP_Q8_0) return swamp_launch_gemm_i8(dtype, d_w, d_x, d_y, m, n_rows, n_cols, s);
+  if (x_type != SWAMP_BF16) return SWAMP_EDTYPE;
   if (n_cols % kBK != 0) return SWAMP_ESHAPE;
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n;

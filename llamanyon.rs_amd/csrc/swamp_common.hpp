@@ -106,6 +106,8 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,
 int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x,
                       uint32_t x_type, float *d_y, int m, int n_rows,
                       int n_cols, hipStream_t s);
+int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, float *d_y, int m,
+                         int n_rows, int n_cols, hipStream_t s);
 int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q,
                                size_t n, hipStream_t s);
 int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k,

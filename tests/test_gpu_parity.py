@@ -313,6 +313,57 @@ def test_gemm_rows_tail_and_token_consistency(pkg, orc, torch_dev):
     assert orc.normalized_error(y[m - 1], g, deq, x_fed[m - 1]) <= 2 * TOL
 
 
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("m,rows,cols", [(512, 4096, 4096), (77, 300, 1024), (2048, 512, 4096),
+                                         (256, 1024, 14336), (1, 33, 128)])
+def test_gemm_int8_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
+    """int8 matrix-core GEMM against Q8_0 activations: x is quantized on the
+    device (swamp_quantize_q8_0, byte-identical to the host quantizer), and
+    the oracle multiplies the dequantized Q8_0 activations -- the values the
+    kernel actually consumed."""
+    torch = torch_dev
+    raw = weights(pkg, dtype, rows, cols, mid=m + 5)
+    x = acts(pkg, m, cols, mid=m + 5)
+    say("gemm int8", dtype, m, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, x)
+    d_q = torch.empty(m * cols // 32 * 34, dtype=torch.uint8, device="cuda")
+    pkg.quantize_q8_0(d_x.data_ptr(), F32, d_q.data_ptr(), m * cols, stream(torch))
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(dtype, d_w.data_ptr(), raw.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m, rows,
+              cols, stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.all(np.isfinite(y))
+    xq = pkg.quantize(Q8_0, x)
+    assert np.array_equal(down(d_q), xq)
+    x_fed = orc.dequantize(Q8_0, xq, m * cols).reshape(m, cols)
+    toks = sorted(set([0, m // 2, m - 1] + list(range(max(0, m - 3), m))))
+    ref = orc.forward_linear_batch(dtype, raw, x_fed[toks], rows, cols, 8)
+    deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(y[toks], ref, deq, x_fed[toks]) <= TOL
+
+
+def test_gemm_int8_argument_errors(pkg, torch_dev):
+    torch = torch_dev
+    rows, cols, m = 64, 192, 8   # 192 is a multiple of 64 but not of 128
+    raw = weights(pkg, Q4_0, rows, cols)
+    d_w = up(torch, raw)
+    d_q = torch.zeros(m * cols // 32 * 34, dtype=torch.uint8, device="cuda")
+    d_y = torch.zeros((m, rows), dtype=torch.float32, device="cuda")
+    with pytest.raises(pkg.GpuError) as e:
+        pkg.qgemm(Q4_0, d_w.data_ptr(), raw.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m, rows,
+                  cols, stream(torch))
+    assert e.value.code == pkg.ESHAPE
+    rawk = weights(pkg, Q4_K, rows, 256)
+    d_wk = up(torch, rawk)
+    with pytest.raises(pkg.GpuError) as e:
+        pkg.qgemm(Q4_K, d_wk.data_ptr(), rawk.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m,
+                  rows, 256, stream(torch))
+    assert e.value.code == pkg.EDTYPE
+    torch.cuda.synchronize()
+    assert np.all(down(d_y) == 0)  # nothing written on error
+
+
 # ------------------------------------------------------ activation quantizer
 
 @pytest.mark.parametrize("x_type", [F32, BF16])

@@ -27,7 +27,10 @@ Also reported (outside the timed steps):
     dot), restated in C, timed on this host's cores on one step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--no-prefill] [--cpu-threads T]
+                       [--no-prefill] [--cpu-threads T] [--sweep]
+--sweep adds one JSON line per extra workload after the main line: the
+Q4_K small-batch sweep (1/4/8/16 tokens) at 8B shapes and the 70B layer
+(decode and 4096-token prefill).
 """
 from __future__ import annotations
 
@@ -117,6 +120,94 @@ def cpu_baseline(pkg, n_threads, min_seconds=10.0):
     }
 
 
+SWEEP_8B = [("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up", 28672, 4096),
+            ("down", 4096, 14336), ("lm_head", 128256, 4096)]
+SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 8192),
+             ("down", 8192, 28672), ("lm_head", 128256, 8192)]
+
+
+def run_sweep(pkg, torch, np, stream, lib):
+    """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
+    (lm_head Q8_0) for 1, 4, 8 and 16 tokens, and the 70B Q4_K layer as
+    batch-1 decode and as a 4096-token bf16 prefill GEMM.  Each matrix is
+    timed alone: 20 launches over 3 rotated weight copies behind a GPU
+    sleep; GB/s over the algorithmic bytes, TFLOP/s over 2*M*rows*K."""
+    s = stream.cuda_stream
+    bpw = {pkg.Q4_0: 18 / 32, pkg.Q4_K: 144 / 256, pkg.Q8_0: 34 / 32}
+
+    def timed(fn, reps=20):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    def weights_dev(dt, rows, k, seed, sigma, copies):
+        raw = pkg.synth_quantized(dt, seed, sigma, rows, k)
+        d0 = torch.from_numpy(raw).cuda()
+        return [d0] + [d0.clone() for _ in range(copies - 1)]
+
+    def check(rc, what):
+        if rc != 0:
+            raise pkg.GpuError(rc, what)
+
+    for label, shapes, sigma in (("llama3-8b", SWEEP_8B, 0.02), ("llama3-70b", SWEEP_70B, 0.015)):
+        for n_tok in ((1, 4, 8, 16) if label == "llama3-8b" else (1,)):
+            per, tot_b, tot_us = [], 0, 0.0
+            for i, (name, rows, k) in enumerate(shapes):
+                dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
+                copies = max(2, min(8, int(2 * 256e6 // (rows * k * bpw[dt])) + 1))
+                ws = weights_dev(dt, rows, k, SEED ^ 0x300 ^ i, sigma, copies)
+                x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x400 ^ i, 1.0, n_tok, k)).cuda()
+                y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+                if n_tok == 1:
+                    fn = lambda c: check(lib.swamp_qgemv(dt, ws[c % copies].data_ptr(), ws[0].numel(),
+                                                         x.data_ptr(), y.data_ptr(), rows, k, s),
+                                         "swamp_qgemv")
+                else:
+                    fn = lambda c: check(lib.swamp_qgemv_batched(
+                        dt, ws[c % copies].data_ptr(), ws[0].numel(), x.data_ptr(), y.data_ptr(),
+                        n_tok, rows, k, 0, s), "swamp_qgemv_batched")
+                us = timed(fn)
+                b = int(rows * k * bpw[dt]) + n_tok * k * 4 + n_tok * rows * 4
+                per.append({"name": name, "dtype": "Q8_0" if dt == pkg.Q8_0 else "Q4_K",
+                            "rows": rows, "k": k, "us": round(us, 2),
+                            "GB/s": round(b / us / 1e3, 1),
+                            "TFLOP/s": round(2 * n_tok * rows * k / us / 1e6, 2)})
+                tot_b += b
+                tot_us += us
+                del ws, x, y
+            print(json.dumps({"sweep": f"{label} decode/small-batch Q4_K (lm_head Q8_0)",
+                              "n_tok": n_tok, "alg_bytes": tot_b, "us": round(tot_us, 1),
+                              "GB/s": round(tot_b / tot_us / 1e3, 1),
+                              "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                              "matrices": per}), flush=True)
+    # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights
+    m = 4096
+    per = []
+    for i, (name, rows, k) in enumerate(SWEEP_70B[:4]):
+        ws = weights_dev(pkg.Q4_K, rows, k, SEED ^ 0x500 ^ i, 0.015, 1)
+        xb = torch.from_numpy(pkg.to_bf16_bits(
+            pkg.fill_normal(SEED ^ 0x600 ^ i, 1.0, m, k)).view(np.int16)).cuda()
+        y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+        fn = lambda c: check(lib.swamp_qgemm(pkg.Q4_K, ws[0].data_ptr(), ws[0].numel(),
+                                             xb.data_ptr(), pkg.BF16, y.data_ptr(), m, rows, k,
+                                             s), "swamp_qgemm")
+        us = timed(fn, reps=5)
+        tf = 2 * m * rows * k / us / 1e6
+        per.append({"name": name, "rows": rows, "k": k, "us": round(us, 1),
+                    "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
+        del ws, xb, y
+    print(json.dumps({"sweep": "llama3-70b prefill Q4_K x bf16, 4096 tokens", "matrices": per}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,6 +218,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=6,
                     help="threads of the CPU baseline (the reference's pool size is 6)")
     ap.add_argument("--copies", type=int, default=3, help="weight-set copies rotated per step")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also print one line per extra workload (8B small-batch Q4_K sweep, "
+                         "70B decode and prefill) after the main line")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -304,6 +398,8 @@ def main():
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)
+    if args.sweep:
+        run_sweep(pkg, torch, np, stream, lib)
 
 
 if __name__ == "__main__":

@@ -242,6 +242,55 @@ def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
     assert orc.normalized_error(y, ref, deq, xs) <= TOL
 
 
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("n_tok,rows,cols", [(2, 77, 320), (5, 33, 64), (12, 16, 8192),
+                                             (16, 3000, 1024), (3, 1, 2304)])
+def test_batched_ragged(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
+    """Row counts that end inside a 16-row tile, K that ends inside a K
+    group (Q4_K rounds cols up to its 256 block), single-row matrices."""
+    torch = torch_dev
+    if dtype == Q4_K:
+        cols = (cols + 255) // 256 * 256
+    raw = weights(pkg, dtype, rows, cols, mid=n_tok + 40)
+    xs = acts(pkg, n_tok, cols, mid=n_tok + 40)
+    say("batched ragged", dtype, n_tok, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, xs)
+    d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv_batched(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                      rows, cols, False, stream(torch))
+    torch.cuda.synchronize()
+    ref = orc.forward_linear_batch(dtype, raw, xs, rows, cols, 8)
+    deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
+    assert orc.normalized_error(down(d_y), ref, deq, xs) <= TOL
+
+
+def test_batched_repeat_bitwise(pkg, torch_dev):
+    """Split-K tiles combine in a fixed order through per-tile counters that
+    each launch leaves at zero: repeated calls, with other shapes (and a
+    larger workspace) in between, give bit-identical results."""
+    torch = torch_dev
+    shapes = [(Q4_K, 16, 4096, 14336), (Q8_0, 7, 6144, 4096), (Q4_0, 16, 300, 4096)]
+    first = []
+    bufs = []
+    for i, (dt, n_tok, rows, cols) in enumerate(shapes):
+        raw = weights(pkg, dt, rows, cols, mid=90 + i)
+        xs = acts(pkg, n_tok, cols, mid=90 + i)
+        bufs.append((dt, n_tok, rows, cols, up(torch, raw), raw.size, up(torch, xs)))
+    say("batched repeat", len(shapes))
+    for rep in range(3):
+        for j, (dt, n_tok, rows, cols, d_w, wl, d_x) in enumerate(bufs):
+            d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+            pkg.qgemv_batched(dt, d_w.data_ptr(), wl, d_x.data_ptr(), d_y.data_ptr(), n_tok, rows,
+                              cols, False, stream(torch))
+            torch.cuda.synchronize()
+            y = down(d_y)
+            assert np.isfinite(y).all()
+            if rep == 0:
+                first.append(y)
+            else:
+                assert np.array_equal(y.view(np.uint32), first[j].view(np.uint32)), (rep, j)
+
+
 @pytest.mark.parametrize("cols", [4096, 14336])
 def test_batched_accumulate(pkg, orc, torch_dev, cols):
     """accumulate=1 is the kernel contract of fused_gemv_q4k_batched

@@ -10,27 +10,26 @@
 // tokens, with enough bytes in flight per CU to cover HBM latency.
 //  * V_MFMA_F32_16X16X32_F16 with A = activations (16 tokens x 32 k) and
 //    B = weights (32 k x 16 rows); C = 16 tokens x 16 rows, 4 VGPRs.
-//  * Work unit = one 16-row tile x one K group (K_g columns).  Every wave
-//    runs its own units from start to end: no reduction across waves, no
-//    barrier in the main loop.  Lane (r = l%16, g = l/16) reads items
-//    g, g+4, g+8, ... (64 weights each) of row r.
-//  * The K group's activations sit in LDS for the whole kernel, rounded to
-//    fp16 and stored in MFMA fragment order: one ds_read_b128 per lane and
-//    step.  The k order inside each MFMA is permuted so that a lane's 8
-//    weights come from ONE nibble dword (Q4) or two int8 dwords (Q8_0); the
-//    activation fragments use the same permutation.
+//  * One workgroup of 16 waves per CU.  Its waves form Wt tile lanes x Wk
+//    K slices (Wt * Wk = 16): Wk = 1 for matrices with many tiles (each
+//    wave streams whole rows), up to 16 for the small ones, so that every
+//    CU has weight bytes in flight.  Lane (r = l%16, g = l/16) of a wave
+//    reads items g, g+4, g+8, ... (64 weights each) of row r in its slice.
+//  * Activations are staged in LDS, rounded to fp16 and stored in MFMA
+//    fragment order: one ds_read_b128 per lane and step.  The k order inside
+//    each MFMA is permuted so that a lane's 8 weights come from ONE nibble
+//    dword (Q4) or two int8 dwords (Q8_0); the staged activations use the
+//    same permutation.  When K x tokens exceeds 128 KB of LDS, K runs in
+//    phases, restaged between barriers, while the accumulators of up to 2
+//    tiles per wave stay in registers.
 //  * Weight bytes stream through buffer loads (one descriptor per tile, the
 //    chunk offset in an SGPR) into two register chunks: chunk s+1 is in
 //    flight while chunk s is dequantized (nibble -> fp16 1024+q with one
 //    and-or per pair, packed fp16 offset and scale) and multiplied.
-//  * K groups of one tile combine through a workspace: each writes its
-//    16x16 partial, bumps the tile's counter, and the group that arrives
-//    last sums the partials in K order (deterministic: 0 + p0 + p1 + ...),
-//    writes y and resets the counter for the next launch.  With one K group
-//    y is written directly.
+//  * With Wk > 1 the K slices of a tile are summed through LDS in slice
+//    order (deterministic) after a barrier; nothing crosses workgroups.
 #include <cstdlib>
 #include <mutex>
-#include <vector>
 
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
@@ -44,11 +43,13 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;       // waves per workgroup
+constexpr int kWaves = 16;      // waves per workgroup, one workgroup per CU
 constexpr int kThreads = kWaves * 64;
 constexpr int kTok = 16;        // tokens per pass (MFMA M)
 constexpr int kRowsTile = 16;   // rows per tile (MFMA N)
-constexpr int kLdsBytes = 65536;  // activation bytes per workgroup: 2 workgroups per CU
+constexpr int kJmax = 2;        // tiles per wave whose accumulators stay in registers
+constexpr int kXLdsMax = 131072;             // activation bytes in LDS (one K phase)
+constexpr int kSlotBytes = kWaves * 16 * 16 * 4;  // one 16x16 fp32 partial per wave
 constexpr uint32_t kF16Magic = 0x64006400u;  // fp16 pair (1024, 1024)
 constexpr uint32_t kOob = 0x80000000u;       // buffer offset past any descriptor: reads 0
 
@@ -229,285 +230,298 @@ struct Args {
   const uint8_t *w;
   const float *x;
   float *y;
-  float *part;     // [n_tiles][kgroups][256] partial tiles (kgroups > 1)
-  int *cnt;        // [n_tiles] arrival counters, zero between launches
   int n_tok, n_rows, n_cols;
   uint32_t row_bytes;
   int ipr;         // items (64 weights) per row
-  int ipg;         // items per K group (multiple of 4 * kChunk)
-  int kgroups;     // K groups per tile
-  int wpg;         // workgroups per K group
+  int ipw;         // items per wave and phase (multiple of 4 * kChunk)
+  int lwk;         // log2 of Wk, the waves that share one tile (K slices)
+  int phases;      // K phases; phase p covers items [p*ipp, p*ipp + ipp), ipp = ipw * Wk
   int accumulate;  // y += W x instead of y = W x
 };
 
-// y[4g+i][row0 + r16] for the tokens and rows that exist.
-__device__ __forceinline__ void write_y(const Args &a, int row0, int r16, int g, float4_t v) {
-  const int row = row0 + r16;
-  if (row >= a.n_rows) return;
+// y[t][row0 + r] += / = v for the tokens and rows that exist.
+__device__ __forceinline__ void put_y(const Args &a, int t, int row, float v) {
+  if (t < a.n_tok && row < a.n_rows) {
+    float *d = a.y + size_t(t) * a.n_rows + row;
+    *d = a.accumulate ? *d + v : v;
+  }
+}
+
+// Workgroup barrier that orders LDS only: the weight loads in flight and
+// the y stores need not drain (__syncthreads would wait for the stores and,
+// the memory counter being in order, for every load issued before them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Stage the activations of items [item0, item0 + n_items) into LDS: entry
+// e = (item, step, token) with the token fastest, so the LDS writes are
+// linear; missing tokens and items past the row are zero.  kU entries per
+// thread are loaded before any is written, so the loads overlap (fewer
+// inside the main loop, where both weight chunks hold registers).
+template <int DT, int TOK, int kU>
+__device__ __forceinline__ void stage_x(const Args &a, half8_t *xl, int item0, int n_items, int tid) {
+  const int n_ent = n_items * 8 * TOK;
+  for (int e0 = tid; e0 < n_ent; e0 += kU * kThreads) {
+    float4 v0[kU], v1[kU];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int t = 4 * g + i;
-    if (t < a.n_tok) {
-      float *d = a.y + size_t(t) * a.n_rows + row;
-      *d = a.accumulate ? *d + v[i] : v[i];
+    for (int u = 0; u < kU; u++) {
+      const int e = e0 + u * kThreads;
+      const int tok = e % TOK, st = (e / TOK) & 7, item = item0 + e / (8 * TOK);
+      v0[u] = v1[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < n_ent && tok < a.n_tok && item < a.ipr) {
+        const float *xp = a.x + size_t(tok) * a.n_cols + size_t(item) * 64;
+        v0[u] = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 0));
+        v1[u] = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 4));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int e = e0 + u * kThreads;
+      if (e < n_ent) {
+        const float v[8] = {v0[u].x, v0[u].y, v0[u].z, v0[u].w, v1[u].x, v1[u].y, v1[u].z, v1[u].w};
+        half8_t h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = _Float16(v[slot_local<DT>(i)]);
+        xl[e] = h;
+      }
     }
   }
 }
 
-// Finish a unit: store (one K group) or partial + counter + fix-up.
-//
-// The partials and counters are shared across XCDs, whose L2 caches are not
-// coherent with each other.  Agent-scope fences would write back and
-// invalidate the whole L2 once per unit; instead every access to shared
-// data is an agent-scope atomic (partials: relaxed stores and loads that
-// are coherent device-wide), and the order "partials complete, then the
-// counter moves" comes from waiting for the stores to complete before the
-// counter's read-modify-write is issued.  The group whose increment returns
-// kgroups-1 therefore finds every other partial already written.
-__device__ __forceinline__ void finish_unit(const Args &a, int tile, int kg, int lane, float4_t acc) {
-  const int r16 = lane & 15, g = lane >> 4;
-  if (a.kgroups == 1) {
-    write_y(a, tile * kRowsTile, r16, g, acc);
-    return;
-  }
-  float *tile_part = a.part + size_t(tile) * a.kgroups * 256;
-  float *mine = tile_part + kg * 256 + lane * 4;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    __hip_atomic_store(mine + i, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed
-  int old = 0;
-  if (lane == 0)
-    old = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __builtin_amdgcn_readfirstlane(old);
-  if (old != a.kgroups - 1) return;
-  // sum in K order, 8 partials' loads in flight at a time
-  float4_t s = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < a.kgroups; k0 += 8) {
-    float v[8][4];
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-      const float *p = tile_part + (k0 + kk) * 256 + lane * 4;
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        v[kk][i] = k0 + kk < a.kgroups
-                       ? __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : 0.f;
-    }
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) s[i] += v[kk][i];
-  }
-  write_y(a, tile * kRowsTile, r16, g, s);
-  if (lane == 0) __hip_atomic_store(a.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Position of a chunk in a wave's sequence: tile batch, K phase, tile in
+// the batch, chunk in the wave's K slice.
+struct Pos {
+  int batch, p, j, c;
+};
 
-// Workgroup b serves K group b % kgroups; its waves take that group's tiles
-// round-robin.  TOK = tokens held in LDS (4, 8 or 16; lanes of larger token
-// index read a duplicate, their C rows are discarded).  kChunk = items per
-// lane in one register chunk.
-template <int DT, int TOK, int kChunk>
-__global__ void __launch_bounds__(kThreads, 2) gemv_batched_kernel(Args a) {
-  extern __shared__ half8_t xl[];  // [ipg][8 steps][TOK] fragments
+// Workgroup b owns tile groups b, b + G, b + 2G, ... (G = gridDim.x); tile
+// group q is tiles q*Wt .. q*Wt + Wt-1, one per tile lane.  Wave w is tile
+// lane w / Wk and K slice w % Wk.  Tile groups are taken kJmax at a time
+// (a batch); per batch the K phases run in order and, inside each, the
+// batch's tiles, so each tile's accumulator stays in registers across
+// phases.  All waves of a workgroup run the same sequence, which keeps the
+// barriers (phase staging, K-slice reduction) uniform.
+template <int DT, int TOK, int kChunk, bool kRagged>
+__global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
+  extern __shared__ half8_t xl[];  // [ipp][8 steps][TOK] fragments, then reduction slots
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const int kg = blockIdx.x % a.kgroups;
-  const int wig = (blockIdx.x / a.kgroups) * kWaves + wave;  // wave index in the group
-  const int wstride = a.wpg * kWaves;
+  const int wk = 1 << a.lwk, wt = kWaves >> a.lwk;
+  const int tl = wave >> a.lwk, ks = wave & (wk - 1);
+  const int ipp = a.ipw << a.lwk;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
-  const int my_tiles = wig < n_tiles ? (n_tiles - 1 - wig) / wstride + 1 : 0;
-  const int cpu = a.ipg / (4 * kChunk);  // chunks per unit
-  const int n_chunks = my_tiles * cpu;
+  const int n_tg = (n_tiles + wt - 1) / wt;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int J = (n_tg - 1 - b) / G + 1;  // tile groups of this workgroup (b < n_tg)
+  const int cpw = a.ipw / (4 * kChunk);  // chunks per wave, tile and phase
+  const int n_chunks = a.phases * cpw * J;
+  const int P = a.phases;
   const uint32_t rb = a.row_bytes;
-  // items of this lane in chunk c: item0 + g + 4*(c*kChunk + i); valid while
-  // 4*(c*kChunk + i) < lim
-  const int item0 = kg * a.ipg;
-  const int lim = a.ipr - item0 - g;
-  const uint32_t lane_off = uint32_t(r16) * rb + lane_item_offset<DT>(g) +
-                            uint32_t(item0 / 4) * quad_bytes<DT>();
+  const uint32_t lane_off = uint32_t(r16) * rb + lane_item_offset<DT>(g);
   const uint32_t chunk_bytes = kChunk * quad_bytes<DT>();
+  float *slots = reinterpret_cast<float *>(xl + ipp * 8 * TOK);  // [16 waves][16 tok][16 rows]
 
-  auto issue = [&](Raw<DT> (&r)[kChunk], int s) {
-    // chunk s of this wave: unit s / cpu, chunk s % cpu (s < n_chunks)
-    const int u = s / cpu, c = s - u * cpu;
-    const int row0 = (wig + u * wstride) * kRowsTile;
-    const int nr = min(kRowsTile, a.n_rows - row0);
-    const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
-    const uint32_t soff = uint32_t(c) * chunk_bytes;
+  auto tile_of = [&](int batch, int j) { return (b + (batch * kJmax + j) * G) * wt + tl; };
+  auto batch_len = [&](int batch) { return min(kJmax, J - batch * kJmax); };
+  auto advance = [&](Pos &q) {
+    if (++q.c < cpw) return;
+    q.c = 0;
+    if (++q.j < batch_len(q.batch)) return;
+    q.j = 0;
+    if (++q.p < P) return;
+    q.p = 0;
+    q.batch++;
+  };
+
+  auto issue = [&](Raw<DT> (&r)[kChunk], const Pos &q) {
+    // Tiles past the matrix (the last tile group, the issue past the end)
+    // re-read the last tile, whose results are never stored.  Every term of
+    // the descriptor stays a scalar min/select: a two-sided clamp becomes
+    // v_med3, a VGPR temporary that can alias a register an in-flight load
+    // still writes, and the wait for it drains the prefetch.
+    const int tile = min(tile_of(q.batch, q.j), n_tiles - 1);
+    const int row0 = tile * kRowsTile;
+    // this wave's items in the chunk: base + g + 4*(c*kChunk + i)
+    const int base = q.p * ipp + ks * a.ipw;
+    const int first = base + 4 * q.c * kChunk;  // first item of the chunk
+    const uint32_t soff = uint32_t(base / 4) * quad_bytes<DT>() + uint32_t(q.c) * chunk_bytes;
+    if constexpr (!kRagged) {
+      // ipr is a multiple of 4 * kChunk: a chunk lies wholly inside the
+      // row or wholly past it (then the descriptor has no records and the
+      // loads return zeros); no per-lane select before the loads
+      const int nr = first < a.ipr ? min(kRowsTile, a.n_rows - row0) : 0;
+      const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
 #pragma unroll
-    for (int i = 0; i < kChunk; i++) {
-      const bool ok = 4 * (c * kChunk + i) < lim;
-      const uint32_t voff = ok ? lane_off + uint32_t(i) * quad_bytes<DT>() : kOob;
-      load_item<DT>(r[i], rs, voff, soff, g);
+      for (int i = 0; i < kChunk; i++)
+        load_item<DT>(r[i], rs, lane_off + uint32_t(i) * quad_bytes<DT>(), soff, g);
+    } else {
+      const int nr = min(kRowsTile, a.n_rows - row0);
+      const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
+#pragma unroll
+      for (int i = 0; i < kChunk; i++) {
+        const bool ok = first + 4 * i + g < a.ipr;
+        const uint32_t voff = ok ? lane_off + uint32_t(i) * quad_bytes<DT>() : kOob;
+        load_item<DT>(r[i], rs, voff, soff, g);
+      }
     }
   };
 
   Raw<DT> ra[kChunk], rbuf[kChunk];
-  if (n_chunks > 0) issue(ra, 0);
+  Pos qi{0, 0, 0, 0};  // next chunk to issue
+  issue(ra, qi);
+  advance(qi);
   __builtin_amdgcn_sched_barrier(0);
-
-  // Stage this K group's activations: entry e = (item, step, token) with
-  // the token fastest, so the LDS writes are linear.
-  {
-    const int n_ent = a.ipg * 8 * TOK;
-    for (int e = tid; e < n_ent; e += kThreads) {
-      const int tok = e % TOK, st = (e / TOK) & 7, il = e / (8 * TOK);
-      const int item = item0 + il;
-      half8_t h;
-      if (tok < a.n_tok && item < a.ipr) {
-        const float *xp = a.x + size_t(tok) * a.n_cols + size_t(item) * 64;
-        const float4 v0 = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 0));
-        const float4 v1 = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 4));
-        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = _Float16(v[slot_local<DT>(i)]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++) h[i] = _Float16(0.0f);
-      }
-      xl[e] = h;
-    }
-  }
+  stage_x<DT, TOK, 4>(a, xl, 0, ipp, tid);
   __syncthreads();
-  if (n_chunks == 0) return;
 
-  // LDS fragment of this lane: item g + 4*(c*kChunk + i), step st, token r16
-  const half8_t *xlane = xl + g * 8 * TOK + (r16 % TOK);
-  float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  int u = 0, c = 0;
+  const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * TOK + (r16 % TOK);
+  // accumulators of the batch's tiles (named registers: an indexed array
+  // would live in scratch, whose accesses share the vector memory counter
+  // with the weight prefetch and drain it)
+  float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  Pos qc{0, 0, 0, 0};  // chunk being consumed
+
+  // Result of tile k of a batch: direct stores when a wave owns its tile's
+  // whole K range, else a K-slice reduction through LDS.
+  auto emit_tile = [&](int batch, int k, const float4_t &v) {
+    const int tile = tile_of(batch, k);
+    if (wk == 1) {
+      if (tile < n_tiles) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) put_y(a, 4 * g + i, tile * kRowsTile + r16, v[i]);
+      }
+      return;
+    }
+    float *mine = slots + wave * 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) mine[(4 * g + i) * 16 + r16] = v[i];
+    lds_barrier();
+    for (int o = tid; o < wt * 256; o += kThreads) {
+      const int otl = o >> 8, e = o & 255;
+      const float *src = slots + (otl << a.lwk) * 256 + e;
+      float sum = 0.f;
+      for (int s2 = 0; s2 < wk; s2++) sum += src[s2 * 256];
+      const int otile = (b + (batch * kJmax + k) * G) * wt + otl;
+      if (otile < n_tiles) put_y(a, e >> 4, otile * kRowsTile + (e & 15), sum);
+    }
+    lds_barrier();
+  };
+  auto emit = [&](int batch) {
+    const int jb = batch_len(batch);
+    emit_tile(batch, 0, acc0);
+    if (jb > 1) emit_tile(batch, 1, acc1);
+    acc0 = acc1 = float4_t{0.f, 0.f, 0.f, 0.f};
+  };
 
   auto consume = [&](const Raw<DT> (&r)[kChunk]) {
-    const half8_t *xc = xlane + c * kChunk * 32 * TOK;
+    if (P > 1 && qc.c == 0 && qc.j == 0 && (qc.p | qc.batch) != 0) {
+      lds_barrier();  // every wave is done with the previous phase
+      stage_x<DT, TOK, 1>(a, xl, qc.p * ipp, ipp, tid);
+      lds_barrier();
+    }
+    const half8_t *xc = xlane + qc.c * kChunk * 32 * TOK;
+    float4_t c = acc0;
 #pragma unroll
     for (int i = 0; i < kChunk; i++) {
-      Q4kScales ks{};
-      if constexpr (DT == SWAMP_Q4_K) ks = q4k_item_scales(r[i], g);
+      Q4kScales kq{};
+      if constexpr (DT == SWAMP_Q4_K) kq = q4k_item_scales(r[i], g);
 #pragma unroll
       for (int st = 0; st < 8; st++) {
         const half8_t xa = xc[i * 32 * TOK + st * TOK];
-        const half8_t wb = weights_step<DT>(r[i], st, ks);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, acc, 0, 0, 0);
+        const half8_t wb = weights_step<DT>(r[i], st, kq);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, c, 0, 0, 0);
       }
     }
-    if (++c == cpu) {
-      finish_unit(a, wig + u * wstride, kg, lane, acc);
-      acc = float4_t{0.f, 0.f, 0.f, 0.f};
-      c = 0;
-      u++;
+    acc0 = c;
+    if (qc.c == cpw - 1) {
+      // next tile of the batch into acc0: rotate by the batch length
+      // (selects, not branches: the optimizer turns the branchy form into a
+      // store at a dynamic index, i.e. into scratch memory)
+      const int jb = batch_len(qc.batch);
+      acc0 = jb > 1 ? acc1 : c;
+      acc1 = c;
+      if (qc.j == jb - 1 && qc.p == P - 1) emit(qc.batch);
     }
+    advance(qc);
   };
 
   for (int s = 0;;) {
-    issue(rbuf, s + 1 < n_chunks ? s + 1 : s);
+    issue(rbuf, qi);  // past the end: re-reads the last tile
+    advance(qi);
     __builtin_amdgcn_sched_barrier(0);
     consume(ra);
     if (++s >= n_chunks) break;
-    issue(ra, s + 1 < n_chunks ? s + 1 : s);
+    issue(ra, qi);
+    advance(qi);
     __builtin_amdgcn_sched_barrier(0);
     consume(rbuf);
     if (++s >= n_chunks) break;
   }
 }
 
-__global__ void zero_i32_kernel(int *__restrict__ p, size_t n) {
-  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
-// Per (device, stream) workspace for the K-group partials and counters.
-// Grown on demand (after draining the stream that used the old one); the
-// counters are zeroed once at allocation and by the kernels afterwards.
-struct Workspace {
-  int device;
-  hipStream_t stream;
-  float *part = nullptr;
-  int *cnt = nullptr;
-  size_t part_floats = 0, n_cnt = 0;
-};
-std::mutex g_ws_mu;
-std::vector<Workspace> g_ws;
-
-int get_workspace(hipStream_t s, size_t part_floats, size_t n_cnt, float **part, int **cnt) {
-  const int dev = swamp::device_info().device;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  Workspace *w = nullptr;
-  for (auto &e : g_ws)
-    if (e.device == dev && e.stream == s) w = &e;
-  if (!w) {
-    g_ws.push_back(Workspace{dev, s});
-    w = &g_ws.back();
-  }
-  if (w->part_floats < part_floats || w->n_cnt < n_cnt) {
-    if (w->part || w->cnt) {
-      if (hipStreamSynchronize(s) != hipSuccess) return SWAMP_ELAUNCH;
-      (void)hipFree(w->part);
-      (void)hipFree(w->cnt);
-      w->part = nullptr;
-      w->cnt = nullptr;
-      w->part_floats = w->n_cnt = 0;
-    }
-    const size_t pf = std::max(part_floats, size_t(1) << 16);
-    const size_t nc = std::max(n_cnt, size_t(1) << 12);
-    if (hipMalloc(reinterpret_cast<void **>(&w->part), pf * sizeof(float)) != hipSuccess)
-      return SWAMP_ELAUNCH;
-    if (hipMalloc(reinterpret_cast<void **>(&w->cnt), nc * sizeof(int)) != hipSuccess) {
-      (void)hipFree(w->part);
-      w->part = nullptr;
-      return SWAMP_ELAUNCH;
-    }
-    zero_i32_kernel<<<unsigned((nc + 255) / 256), 256, 0, s>>>(w->cnt, nc);
-    if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
-    w->part_floats = pf;
-    w->n_cnt = nc;
-  }
-  *part = w->part;
-  *cnt = w->cnt;
-  return SWAMP_OK;
-}
-
-template <int DT>
-constexpr int chunk_items() {
-  return DT == SWAMP_Q4_0 ? 4 : 2;  // 144, 136 and 96 bytes per lane and chunk
-}
-
-template <int DT, int TOK>
-int launch_pass_tok(Args a, hipStream_t s) {
-  constexpr int kC = chunk_items<DT>();
-  auto kern = gemv_batched_kernel<DT, TOK, kC>;
+// Launch geometry: tokens in LDS, items per register chunk, waves per tile,
+// K phases.
+template <int DT, int TOK, int kChunk, bool kRagged>
+int launch_geo(Args a, int lwk, hipStream_t s) {
+  auto kern = gemv_batched_kernel<DT, TOK, kChunk, kRagged>;
   static std::once_flag once;
   std::call_once(once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kXLdsMax + kSlotBytes);
   });
+  const int q = 4 * kChunk;                           // item granule of a wave's K slice
+  const int xcap = kXLdsMax / (TOK * 8 * 16);         // items of activations in LDS
+  const int wk = 1 << lwk;
+  const int ipp_max = xcap / (q * wk) * (q * wk);
+  a.phases = (a.ipr + ipp_max - 1) / ipp_max;
+  const int per_phase = (a.ipr + a.phases - 1) / a.phases;
+  const int ipp = (per_phase + q * wk - 1) / (q * wk) * (q * wk);
+  a.ipw = ipp / wk;
+  a.lwk = lwk;
+  const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
+  const int n_tg = (n_tiles + (kWaves >> lwk) - 1) / (kWaves >> lwk);
+  const int grid = std::min(n_tg, swamp::device_info().num_cus);
+  const size_t lds = size_t(ipp) * 8 * TOK * 16 + (wk > 1 ? kSlotBytes : 0);
+  kern<<<unsigned(grid), kThreads, lds, s>>>(a);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
+
+// Waves per tile: the power of two that minimises the estimated time,
+// rounds of tile groups x (K per wave + the K-slice reduction, costed as
+// 1/20 of a full row), the smaller one on ties.
+template <int DT, int TOK>
+int launch_pass_tok(Args a, hipStream_t s) {
   const int cus = swamp::device_info().num_cus;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
-  const int q = 4 * kC;                        // item granule of a K group
-  const int ipg_max = kLdsBytes / (TOK * 16 * 8) / q * q;  // LDS: 128*TOK bytes per item
-  const int granules = (a.ipr + q - 1) / q;
-  // Fewest K groups that fit LDS, then more until the units cover the
-  // wave slots (2 workgroups x 8 waves per CU) or a group is one granule.
-  const int slots = cus * 2 * kWaves;
-  int kgroups = (a.ipr + ipg_max - 1) / ipg_max;
-  while (kgroups < granules && size_t(n_tiles) * kgroups < size_t(slots) * 3 / 4) kgroups++;
-  static const int forced = [] {  // tuning override: SWAMP_BATCHED_KGROUPS
-    const char *e = std::getenv("SWAMP_BATCHED_KGROUPS");
-    return e ? std::atoi(e) : 0;
+  const int xcap = kXLdsMax / (TOK * 8 * 16);
+  static const int forced = [] {  // tuning override: SWAMP_BATCHED_LWK (0..4)
+    const char *e = std::getenv("SWAMP_BATCHED_LWK");
+    return e ? std::atoi(e) : -1;
   }();
-  if (forced > 0) kgroups = std::max((a.ipr + ipg_max - 1) / ipg_max, std::min(forced, granules));
-  int ipg = ((granules + kgroups - 1) / kgroups) * q;
-  kgroups = (a.ipr + ipg - 1) / ipg;
-  a.ipg = ipg;
-  a.kgroups = kgroups;
-  a.wpg = std::max(1, std::min((n_tiles + kWaves - 1) / kWaves, (2 * cus) / kgroups));
-  if (kgroups > 1) {
-    if (int rc = get_workspace(s, size_t(n_tiles) * kgroups * 256, size_t(n_tiles), &a.part, &a.cnt))
-      return rc;
+  int best = 0;
+  double best_cost = 1e30;
+  for (int lwk = 0; lwk <= 4; lwk++) {
+    const int wt = kWaves >> lwk;
+    const int n_tg = (n_tiles + wt - 1) / wt;
+    const int rounds = (n_tg + cus - 1) / cus;
+    const double cost = double(rounds) * (1.0 / double(1 << lwk) + (lwk ? 0.05 : 0.0));
+    if (cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best = lwk;
+    }
   }
-  const size_t lds = size_t(ipg) * 8 * TOK * 16;
-  kern<<<unsigned(kgroups * a.wpg), kThreads, lds, s>>>(a);
-  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+  if (forced >= 0 && forced <= 4) best = forced;
+  // The Wk K slices of one phase hold a granule of 4 * kChunk items each:
+  // two-item chunks when that fits LDS and the row, else one-item chunks,
+  // else fewer slices.
+  while (best > 0 && ((4 << best) > xcap || (4 << best) > a.ipr)) best--;
+  if ((8 << best) <= xcap && (8 << best) <= a.ipr)
+    return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, s) : launch_geo<DT, TOK, 2, false>(a, best, s);
+  return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, best, s) : launch_geo<DT, TOK, 1, false>(a, best, s);
 }
 
 template <int DT>
@@ -528,8 +542,10 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   a.n_rows = n_rows;
   a.n_cols = n_cols;
   a.row_bytes = uint32_t(swamp::row_bytes(int(dtype), size_t(n_cols)));
-  a.ipr = n_cols / 64;
+  a.ipr = (n_cols + 63) / 64;
   a.accumulate = accumulate;
+  // 16 rows of a tile are addressed by one buffer descriptor (32-bit range)
+  if (size_t(a.row_bytes) * kRowsTile >= (size_t(1) << 30)) return SWAMP_ESHAPE;
   for (int t0 = 0; t0 < n_tok; t0 += kTok) {
     a.n_tok = std::min(kTok, n_tok - t0);
     a.x = d_x + size_t(t0) * n_cols;

@@ -27,10 +27,11 @@ Also reported (outside the timed steps):
     dot), restated in C, timed on this host's cores on one step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--no-prefill] [--cpu-threads T] [--sweep]
+                       [--no-prefill] [--cpu-threads T] [--sweep] [--pmc-probe]
 --sweep adds one JSON line per extra workload after the main line: the
 Q4_K small-batch sweep (1/4/8/16 tokens) at 8B shapes and the 70B layer
-(decode and 4096-token prefill).
+(decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
+and a copy of known size, for the rocprofv3 --pmc traffic measurement.
 """
 from __future__ import annotations
 
@@ -221,6 +222,9 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also print one line per extra workload (8B small-batch Q4_K sweep, "
                          "70B decode and prefill) after the main line")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
+                         "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -254,6 +258,28 @@ def main():
     step_bytes = sum(alg_bytes_gemv(18, r, k) for _, r, k in DECODE_SHAPES)
     rotated = sum(t.numel() for st in sets for t in st)
     lib = pkg.gpu_lib()
+
+    if args.pmc_probe:
+        # HBM traffic of the dominant kernel under rocprofv3 --pmc: its
+        # launches (one per weight copy), then a plain copy of known size
+        # whose counter reading calibrates the counter (bytes per unit).
+        i = max(range(len(DECODE_SHAPES)), key=lambda j: DECODE_SHAPES[j][1] * DECODE_SHAPES[j][2])
+        _, rows, k = DECODE_SHAPES[i]
+        for it in range(5):
+            w = sets[it % args.copies][i]
+            rc = lib.swamp_qgemv(pkg.Q4_0, w.data_ptr(), w.numel(), xs[i].data_ptr(),
+                                 ys[i].data_ptr(), rows, k, s)
+            if rc != 0:
+                raise pkg.GpuError(rc, "swamp_qgemv")
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"pmc probe: 5 x swamp_qgemv Q4_0 {rows}x{k} "
+              f"({alg_bytes_gemv(18, rows, k)} algorithmic bytes each), then a "
+              f"{src.numel()}-byte device copy", flush=True)
+        return
 
     def launch(c, i):
         _, rows, k = DECODE_SHAPES[i]

@@ -10,12 +10,14 @@
 //  * Workgroup tile 256 tokens x 256 weight rows, K step 64, 4 waves in a
 //    2 x 2 arrangement; each wave owns 128 x 128 outputs = 4 x 4
 //    V_MFMA_F32_32X32X16_BF16 tiles (256 fp32 accumulators per lane).
-//  * Two LDS stages (activations 32 KB + dequantized weights 32 KB each,
-//    128 KB of the 160 KB) and two register stages: the global loads of
-//    K step t+2 are issued while step t computes, and step t+1's bytes
-//    (loaded during step t-1) are dequantized and written into the other
-//    LDS stage in slices interleaved with step t's MFMAs, so the vector
-//    ALU and LDS work hides under the matrix cores.  One barrier per step.
+//  * LDS: three activation stages and two dequantized-weight stages, 32 KB
+//    each (160 KB).  Activations go global -> LDS directly (buffer_load ...
+//    lds, no VGPRs, no LDS write instructions), two K steps ahead; weight
+//    items go to registers two steps ahead and are dequantized one step
+//    ahead into the other weight stage, in slices interleaved with the
+//    current step's MFMAs, so the vector ALU and LDS work hides under the
+//    matrix cores.  One barrier per step, which waits (in-order memory
+//    counter) for the next step's activations only.
 //  * Fragments of the next 16-wide k slice are read from LDS while the
 //    current slice's 16 MFMAs run.
 //  * Weight dequantization: lane t owns row t of the tile; one 64-weight
@@ -25,8 +27,9 @@
 //    32-row fragment reads and the row-wise writes spread over the banks.
 //  * Workgroup ids are remapped so each XCD (ids i, i+8, ...) walks a
 //    contiguous run of tiles that share weight columns in its L2.
-//  * Grids with fewer tiles than CUs split K across workgroups; those add
-//    into y (zeroed first) with hardware float atomics.
+//  * The tiles of an incomplete last round (all tiles, when there are fewer
+//    than CUs) are split along K across workgroups; those add into y
+//    (their blocks zeroed first) with hardware float atomics.
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
 
@@ -36,7 +39,6 @@
 namespace {
 
 using swamp::Raw;
-using swamp::load_raw;
 using swamp::q4k_scales;
 using swamp::shr16;
 
@@ -47,8 +49,10 @@ typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kThreads = 256;
-constexpr int kStageBytes = (kBM + kBN) * kBK * 2;  // 64 KB
-constexpr int kSmemBytes = 2 * kStageBytes;         // 128 KB
+constexpr int kXStage = kBM * kBK * 2;              // 32 KB activations
+constexpr int kWStage = kBN * kBK * 2;              // 32 KB dequantized weights
+constexpr int kXOff = 0, kWOff = 3 * kXStage;        // 3 activation + 2 weight stages
+constexpr int kSmemBytes = 3 * kXStage + 2 * kWStage; // 160 KB
 
 #ifndef SWAMP_GEMM_SWZ
 #define SWAMP_GEMM_SWZ 1
@@ -166,27 +170,31 @@ __device__ __forceinline__ void load_item(Raw<DT> &r, __amdgpu_buffer_rsrc_t rs,
   }
 }
 
-// Per-thread load geometry.  Activation chunk i of a step is row
-// m0 + 32 i + tid/8, 16-byte chunk tid%8 of the step's 128 bytes; rows past
-// M read zeros (descriptor range).  The weight item is row n0 + tid.
+// Per-thread load geometry.  Activations go global -> LDS directly
+// (buffer_load ... lds): instruction i of wave w fills LDS bytes
+// [1024 (8w + i), +1024) of an activation stage = rows 8(8w+i) .. +7, lane L
+// writing row 8(8w+i) + L/8, physical 16-byte chunk L%8; the lane fetches
+// the logical chunk that the swizzle puts there.  The weight item is row
+// n0 + tid, through registers (it is dequantized).
 struct Geo {
   __amdgpu_buffer_rsrc_t xr, wr;
-  uint32_t xv, wv;  // per-lane VGPR offsets
+  uint32_t xv[2];   // per-lane VGPR offsets for even / odd instructions
   uint32_t xs;      // m0 * K * 2 (scalar)
-  uint32_t xrow;    // 32 * K * 2: scalar step between chunks i
-  int xoff[8];      // LDS byte offsets of the chunks (swizzled)
+  uint32_t xinst;   // 8 * K * 2: scalar step between instructions
+  uint32_t wv;      // per-lane weight row offset
+  int wave;
 };
 
-__device__ __forceinline__ void xload(u32x4v_t (&xb)[8], const Geo &g, int kt) {
+__device__ __forceinline__ void xdma(uint8_t *xstage, const Geo &g, int kt) {
 #pragma unroll
   for (int i = 0; i < 8; i++)
-    xb[i] = __builtin_amdgcn_raw_buffer_load_b128(g.xr, g.xv,
-                                                 g.xs + uint32_t(i) * g.xrow + uint32_t(kt) * 128u, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        g.xr, (__attribute__((address_space(3))) void *)(xstage + 1024 * (8 * g.wave + i)), 16,
+        g.xv[i & 1], g.xs + uint32_t(i) * g.xinst + uint32_t(kt) * 128u, 0, 0);
 }
 
-__device__ __forceinline__ void frags(const uint8_t *stg, int ks, int wm, int wn, int lane,
-                                      bf16x8_t (&a)[4], bf16x8_t (&b)[4]) {
-  const uint8_t *ws = stg + kBM * kBK * 2;
+__device__ __forceinline__ void frags(const uint8_t *stg, const uint8_t *ws, int ks, int wm, int wn,
+                                      int lane, bf16x8_t (&a)[4], bf16x8_t (&b)[4]) {
   const int fr = lane & 31, fc = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 4; i++)
@@ -196,49 +204,34 @@ __device__ __forceinline__ void frags(const uint8_t *stg, int ks, int wm, int wn
     b[j] = *reinterpret_cast<const bf16x8_t *>(ws + swz(wn * 128 + j * 32 + fr, 2 * ks + fc));
 }
 
-// Register stage of one K step: its 8 activation chunks and weight item.
 template <int DT>
-struct Stage {
-  u32x4v_t x[8];
-  Raw<DT> w;
-};
-
-template <int DT>
-__device__ __forceinline__ void sload(Stage<DT> &st, const Geo &g, int kt) {
-  xload(st.x, g, kt);
-  load_item<DT>(st.w, g.wr, g.wv, kt);
+__host__ __device__ constexpr int wloads() {
+  return DT == SWAMP_Q8_0 ? 5 : 3;  // buffer loads per weight item
 }
 
-// One K step on LDS stage `cur`: 4 slices of 16 MFMAs.  Meanwhile step
-// kt+1 (registers `nx`, loaded during step kt-1) goes to LDS stage `nxt`
-// -- its activations at once, its weights dequantized two chunks per
-// slice -- and step kt+2's global loads land in `fetch`.  Within a slice the
-// scheduler is told to alternate one MFMA with three other VALU
-// instructions, so the vector work runs in the MFMAs' shadow (a wave
-// issues in order: a run of MFMAs stalls it while the matrix pipe is busy,
-// a run of VALU leaves the matrix pipe idle).
+// One K step: MFMAs on activation stage xc and weight stage wc.  Meanwhile
+// step kt+2's activations stream into stage xf by DMA and its weight item
+// into registers `fetch`; step kt+1's weight item (registers `nw`, loaded a
+// step ago) is dequantized into weight stage wn.  The closing barrier waits
+// (in-order memory counter) for step kt+1's DMA only: the loads issued
+// after it -- kt+1's weights, kt+2's DMA and weights -- stay in flight.
 template <int DT>
-__device__ __forceinline__ void kstep(f32x16_t (&acc)[4][4], const uint8_t *cur, uint8_t *nxt,
-                                      const Stage<DT> &nx, Stage<DT> &fetch, const Geo &g,
-                                      int kt, int kt1, int tid) {
+__device__ __forceinline__ void kstep(f32x16_t (&acc)[4][4], const uint8_t *xc, const uint8_t *wc,
+                                      uint8_t *xf, uint8_t *wn, const Raw<DT> &nw,
+                                      Raw<DT> &fetch, const Geo &g, int kt, int kt1, int tid) {
   const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn_ = wave >> 1;
   const int k1 = min(kt + 1, kt1 - 1), k2 = min(kt + 2, kt1 - 1);  // past the end: re-read
-  sload<DT>(fetch, g, k2);
-  // keep the loads at the top of the step (the scheduler would sink them
-  // next to their first use and expose their latency)
+  xdma(xf, g, k2);
   __builtin_amdgcn_sched_barrier(0);
-  // step kt+1's activations (loaded a step ago) go to LDS first, freeing
-  // their registers for the rest of the step
-#pragma unroll
-  for (int c = 0; c < 8; c++) *reinterpret_cast<u32x4v_t *>(nxt + g.xoff[c]) = nx.x[c];
-  uint8_t *ws = nxt + kBM * kBK * 2;
+  load_item<DT>(fetch, g.wr, g.wv, k2);
+  __builtin_amdgcn_sched_barrier(0);
   bf16x8_t a[2][4], b[2][4];
-  frags(cur, 0, wm, wn, lane, a[0], b[0]);
+  frags(xc, wc, 0, wm, wn_, lane, a[0], b[0]);
 #pragma unroll
   for (int ks = 0; ks < 4; ks++) {
     const int p = ks & 1;
-    if (ks < 3) frags(cur, ks + 1, wm, wn, lane, a[p ^ 1], b[p ^ 1]);
+    if (ks < 3) frags(xc, wc, ks + 1, wm, wn_, lane, a[p ^ 1], b[p ^ 1]);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -247,7 +240,7 @@ __device__ __forceinline__ void kstep(f32x16_t (&acc)[4][4], const uint8_t *cur,
 #pragma unroll
     for (int q = 0; q < 2; q++) {
       const int c = 2 * ks + q;
-      *reinterpret_cast<u32x4v_t *>(ws + swz(tid, c)) = dequant_chunk<DT>(nx.w, k1, c);
+      *reinterpret_cast<u32x4v_t *>(wn + swz(tid, c)) = dequant_chunk<DT>(nw, k1, c);
     }
 #pragma unroll
     for (int m = 0; m < 16; m++) {
@@ -256,42 +249,67 @@ __device__ __forceinline__ void kstep(f32x16_t (&acc)[4][4], const uint8_t *cur,
       if (m < 8 && ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
       if (m == 9 || m == 13) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // 1 DS write
     }
-    // slice boundary: the next slice's fragment reads stay in this slice
     __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
+  // wait for step kt+1's DMA (8 + 2 weight loads were issued after it)
+  constexpr int kAfter = 8 + 2 * wloads<DT>();
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kAfter) : "memory");
 }
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(
     const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, float *__restrict__ y, int M,
-    int N, int K, size_t row_bytes, int tiles_m, int tiles_n, int kt_per_split, int atomic) {
+    int N, int K, size_t row_bytes, int tiles_m, int n_full, int splits, int kt_per_split) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave & 1, wn = wave >> 1;
 
-  // XCD-aware tile order: hardware ids i, i+8, ... run on one XCD; give
-  // each XCD a contiguous slice of the (m-fastest) tile sequence, so the
-  // M tiles sharing a weight column share that XCD's L2.
-  const int tiles = tiles_m * tiles_n;
-  const int total = tiles * int(gridDim.y);
-  int L = blockIdx.x + blockIdx.y * gridDim.x;
-  if (total % 8 == 0) L = (L % 8) * (total / 8) + L / 8;
-  const int split = L / tiles, tile = L % tiles;
+  // Work items: tiles [0, n_full) with their whole K range, then `splits`
+  // K pieces of each remaining tile (added into y atomically; their y
+  // blocks are zeroed first).  XCD-aware order: hardware ids i, i+8, ...
+  // run on one XCD; each XCD gets a contiguous run of the (m-fastest) full
+  // tiles -- M tiles sharing a weight column share that XCD's L2 -- and an
+  // equal share of the pieces, which come last on every XCD.
+  const int n_work = int(gridDim.x);
+  const int n_piece = n_work - n_full;
+  int L = blockIdx.x;
+  if (n_full % 8 == 0 && n_piece % 8 == 0) {
+    const int xcd = L % 8, loc = L / 8, f8 = n_full / 8, p8 = n_piece / 8;
+    L = loc < f8 ? xcd * f8 + loc : n_full + xcd * p8 + (loc - f8);
+  }
+  const int KT = K / kBK;
+  int tile, kt0, kt1, atomic;
+  if (L < n_full) {
+    tile = L;
+    kt0 = 0;
+    kt1 = KT;
+    atomic = 0;
+  } else {
+    const int q = L - n_full;
+    tile = n_full + q / splits;
+    kt0 = (q % splits) * kt_per_split;
+    kt1 = min(KT, kt0 + kt_per_split);
+    atomic = 1;
+  }
   const int mt = tile % tiles_m, nt = tile / tiles_m;
   const int m0 = mt * kBM, n0 = nt * kBN;
-  const int KT = K / kBK;
-  const int kt0 = split * kt_per_split;
-  const int kt1 = min(KT, kt0 + kt_per_split);
 
   Geo g;
+  g.wave = __builtin_amdgcn_readfirstlane(wave);
   g.xr = swamp::make_rsrc(x, uint32_t(size_t(M) * K * 2));
-  g.xv = uint32_t(((tid >> 3) * K + 8 * (tid & 7)) * 2);
-  g.xs = uint32_t(size_t(m0) * K * 2);
-  g.xrow = uint32_t(32 * K * 2);
+  {
+    // lane L of instruction i: row 8(8w+i) + L/8, physical chunk L%8,
+    // logical chunk (L%8) ^ ((row >> 1) & 7) = (L%8) ^ ((4i + L/16) & 7)
+    const int rl = wave * 64 + (lane >> 3);
 #pragma unroll
-  for (int i = 0; i < 8; i++) g.xoff[i] = swz(i * 32 + (tid >> 3), tid & 7);
+    for (int par = 0; par < 2; par++) {
+      const int c = (lane & 7) ^ ((4 * par + (lane >> 4)) & 7);
+      g.xv[par] = uint32_t((rl * K + 8 * c) * 2);
+    }
+  }
+  g.xs = uint32_t(size_t(m0) * K * 2);
+  g.xinst = uint32_t(8 * K * 2);
   const int nrows = min(kBN, N - n0);
   g.wr = swamp::make_rsrc(w + size_t(n0) * row_bytes, uint32_t(size_t(nrows) * row_bytes));
   g.wv = uint32_t(size_t(tid) * row_bytes);
@@ -304,31 +322,40 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  Stage<DT> s0, s1;
-  uint8_t *const st0 = smem, *const st1 = smem + kStageBytes;
-  // prologue: step kt0 into LDS stage 0, step kt0+1 in registers
-  sload<DT>(s0, g, kt0);
-  sload<DT>(s1, g, min(kt0 + 1, kt1 - 1));
-  {
-    uint8_t *ws = st0 + kBM * kBK * 2;
+  uint8_t *const X0 = smem + kXOff, *const W0 = smem + kWOff;
+  auto xst = [&](int s) { return X0 + kXStage * s; };
+  auto wst = [&](int s) { return W0 + kWStage * s; };
+  Raw<DT> r0, r1;
+  // prologue: step kt0 -> X0 (DMA) and W0 (dequant); kt0+1 -> X1 (DMA) and r1
+  xdma(xst(0), g, kt0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_item<DT>(r0, g.wr, g.wv, kt0);
+  __builtin_amdgcn_sched_barrier(0);
+  xdma(xst(1), g, min(kt0 + 1, kt1 - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  load_item<DT>(r1, g.wr, g.wv, min(kt0 + 1, kt1 - 1));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-      *reinterpret_cast<u32x4v_t *>(st0 + g.xoff[c]) = s0.x[c];
-      *reinterpret_cast<u32x4v_t *>(ws + swz(tid, c)) = dequant_chunk<DT>(s0.w, kt0, c);
-    }
+  for (int c = 0; c < 8; c++)
+    *reinterpret_cast<u32x4v_t *>(wst(0) + swz(tid, c)) = dequant_chunk<DT>(r0, kt0, c);
+  {
+    // step kt0's DMA done: kt0's weights, kt0+1's DMA and weights follow it
+    constexpr int kAfter = 8 + 2 * wloads<DT>();
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kAfter) : "memory");
   }
-  __syncthreads();
 
-  // Two steps per trip so the register stages keep static roles (a copy
-  // between them would wait for the in-flight loads); the odd last step
-  // runs after the loop (a break inside the trip made the register
-  // allocator spill).
+  // Two steps per trip (static register roles); LDS stages rotate with the
+  // step: activations kt%3, weights kt%2 (counted from kt0).
   int kt = kt0;
   for (; kt + 1 < kt1; kt += 2) {
-    kstep<DT>(acc, st0, st1, s1, s0, g, kt, kt1, tid);
-    kstep<DT>(acc, st1, st0, s0, s1, g, kt + 1, kt1, tid);
+    const int j = kt - kt0;
+    kstep<DT>(acc, xst(j % 3), wst(0), xst((j + 2) % 3), wst(1), r1, r0, g, kt, kt1, tid);
+    kstep<DT>(acc, xst((j + 1) % 3), wst(1), xst((j + 3) % 3), wst(0), r0, r1, g, kt + 1, kt1, tid);
   }
-  if (kt < kt1) kstep<DT>(acc, st0, st1, s1, s0, g, kt, kt1, tid);
+  if (kt < kt1) {
+    const int j = kt - kt0;
+    kstep<DT>(acc, xst(j % 3), wst(0), xst((j + 2) % 3), wst(1), r1, r0, g, kt, kt1, tid);
+  }
 
   // C layout of a 32x32 tile: lane holds column (lane & 31), rows
   // 8*(e/4) + 4*(lane/32) + (e%4) for e = 0..15.
@@ -350,9 +377,18 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(
     }
 }
 
-__global__ void zero_f32_kernel(float *__restrict__ p, size_t n) {
-  const size_t stride = size_t(gridDim.x) * blockDim.x;
-  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+// Zero the y blocks of tiles [first, first + gridDim.x / 64): block b
+// clears 4 rows of tile first + b/64, each thread 4 consecutive floats.
+__global__ void zero_tiles_kernel(float *__restrict__ y, int M, int N, int tiles_m, int first) {
+  const int tile = first + int(blockIdx.x) / 64;
+  const int mt = tile % tiles_m, nt = tile / tiles_m;
+  const int m = mt * kBM + 4 * (int(blockIdx.x) % 64) + int(threadIdx.x) / 64;
+  const int n = nt * kBN + 4 * (int(threadIdx.x) % 64);
+  if (m >= M) return;
+  float *row = y + size_t(m) * N;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    if (n + i < N) row[n + i] = 0.f;
 }
 
 // ---- Q8_0 activation quantization ------------------------------------------
@@ -409,19 +445,31 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n;
   const int KT = n_cols / kBK;
-  // Split K when the tiles leave CUs idle: as many splits as fit in one
-  // pass over the CUs, each at least 8 K steps long.
+  // Balance the last round over the CUs (one workgroup per CU).  Split
+  // pieces of a tile add into y with float atomics, which cost about as
+  // much as a quarter of a round when every tile of a full round is split
+  // (measured), so: fewer tiles than half the CUs -> every tile splits
+  // along K into min(cus / tiles, 4) pieces; a last round at most half
+  // full -> its tiles split in 2; otherwise no split.  Pieces are at least
+  // 8 K steps long.
   const int cus = swamp::device_info().num_cus;
-  int splits = std::max(1, std::min(cus / std::max(1, tiles), KT / 8));
+  const int rem = tiles % cus;
+  int n_full = tiles, splits = 1;
+  if (tiles * 2 <= cus) {
+    splits = std::min({cus / tiles, 4, KT / 8});
+    n_full = 0;
+  } else if (tiles > cus && rem > 0 && rem * 2 <= cus) {
+    splits = std::min(2, KT / 8);
+    n_full = tiles - rem;
+  }
+  splits = std::max(1, splits);
   const int kt_per_split = (KT + splits - 1) / splits;
   splits = (KT + kt_per_split - 1) / kt_per_split;
-  const int atomic = splits > 1 ? 1 : 0;
-  if (atomic) {
-    const size_t n = size_t(m) * n_rows;
-    zero_f32_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, size_t(cus) * 16)), 256, 0, s>>>(
-        d_y, n);
-  }
-  const dim3 grid{unsigned(tiles), unsigned(splits), 1u};
+  if (splits <= 1) n_full = tiles;
+  const int n_work = n_full + (tiles - n_full) * splits;
+  if (n_full < tiles)
+    zero_tiles_kernel<<<unsigned((tiles - n_full) * 64), 256, 0, s>>>(d_y, m, n_rows, tiles_m, n_full);
+  const dim3 grid{unsigned(n_work), 1u, 1u};
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint16_t *x = static_cast<const uint16_t *>(d_x);
   const size_t rb = swamp::row_bytes(int(dtype), size_t(n_cols));
@@ -430,8 +478,8 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   case DT:                                                                                     \
     if (int rc = set_smem_attr<DT>()) return rc;                                               \
     gemm_bf16_kernel<DT><<<grid, kThreads, kSmemBytes, s>>>(w, x, d_y, m, n_rows, n_cols, rb,  \
-                                                            tiles_m, tiles_n, kt_per_split,    \
-                                                            atomic);                           \
+                                                            tiles_m, n_full, splits,           \
+                                                            kt_per_split);                     \
     break;
     SWAMP_GEMM_CASE(SWAMP_Q4_0)
     SWAMP_GEMM_CASE(SWAMP_Q8_0)

@@ -28,8 +28,9 @@ DTYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K",
 BLOCK = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
 TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
 
-# return codes (include/swamp_qmm.h)
+# return codes (include/swamp_qmm.h, include/swamp_gguf.h)
 OK, EINVAL, EDTYPE, ESHAPE, ELAUNCH, ENODEVICE, EWORKSPACE = 0, -1, -2, -3, -4, -5, -6
+EIO, EMAGIC, EVERSION, ENOTFOUND, ETENSOR = -7, -8, -9, -10, -11
 MULTI_MAX = 8
 
 # Every symbol include/swamp_qmm.h declares.
@@ -38,6 +39,14 @@ GPU_SYMBOLS = (
     "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_multi",
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_quantize_q8_0",
     "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
+)
+# Every symbol include/swamp_gguf.h declares (also in libswamp_gpu.so).
+GGUF_SYMBOLS = (
+    "swamp_gguf_open", "swamp_gguf_close", "swamp_gguf_version", "swamp_gguf_n_tensors",
+    "swamp_gguf_n_kv", "swamp_gguf_data_offset", "swamp_gguf_file_size",
+    "swamp_gguf_tensor_info", "swamp_gguf_find", "swamp_gguf_tensor_raw", "swamp_gguf_upload",
+    "swamp_gguf_meta_type", "swamp_gguf_meta_u32", "swamp_gguf_meta_u64", "swamp_gguf_meta_f32",
+    "swamp_gguf_meta_str",
 )
 QUANT_SYMBOLS = (
     "swamp_f32_to_f16", "swamp_f32_to_bf16", "swamp_f32_to_bf16_array",
@@ -93,6 +102,29 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_quantize_q8_0": (i32, [c_vp, u32, c_vp, c_size, c_vp]),
         "swamp_fused_gemv_q4k": (None, [c_vp, c_vp, c_vp, i32, i32]),
         "swamp_gemv_q8_vnni": (ctypes.c_float, [c_vp, c_vp, i32, ctypes.c_float]),
+        # GGUF reader (include/swamp_gguf.h)
+        "swamp_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(c_vp)]),
+        "swamp_gguf_close": (None, [c_vp]),
+        "swamp_gguf_version": (u32, [c_vp]),
+        "swamp_gguf_n_tensors": (ctypes.c_int64, [c_vp]),
+        "swamp_gguf_n_kv": (ctypes.c_int64, [c_vp]),
+        "swamp_gguf_data_offset": (ctypes.c_uint64, [c_vp]),
+        "swamp_gguf_file_size": (ctypes.c_uint64, [c_vp]),
+        "swamp_gguf_tensor_info": (i32, [c_vp, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p),
+                                         ctypes.POINTER(u32), ctypes.POINTER(i32),
+                                         ctypes.POINTER(ctypes.c_uint64),
+                                         ctypes.POINTER(ctypes.c_uint64),
+                                         ctypes.POINTER(ctypes.c_uint64)]),
+        "swamp_gguf_find": (ctypes.c_int64, [c_vp, ctypes.c_char_p]),
+        "swamp_gguf_tensor_raw": (i32, [c_vp, ctypes.c_int64, ctypes.POINTER(c_vp),
+                                        ctypes.POINTER(c_size)]),
+        "swamp_gguf_upload": (i32, [c_vp, ctypes.c_int64, c_vp, c_size, c_vp]),
+        "swamp_gguf_meta_type": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(u32)]),
+        "swamp_gguf_meta_u32": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(u32)]),
+        "swamp_gguf_meta_u64": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+        "swamp_gguf_meta_f32": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+        "swamp_gguf_meta_str": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                      ctypes.POINTER(c_size)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -229,3 +261,135 @@ def to_bf16_bits(src):
     out = np.empty(src.shape, dtype=np.uint16)
     quant_lib().swamp_f32_to_bf16_array(src.ctypes.data, out.ctypes.data, src.size)
     return out
+
+
+class TensorInfo:
+    """TensorInfo (swamp-gguf/src/tensor_info.rs:8-15): name, shape, dtype and
+    the ABSOLUTE file offset (GgufFile::parse adds the data offset,
+    mmap.rs:81-86), plus nbytes (tensor_info.rs:24-27)."""
+
+    __slots__ = ("index", "name", "shape", "dtype", "offset", "nbytes")
+
+    def __init__(self, index, name, shape, dtype, offset, nbytes):
+        self.index, self.name, self.shape = index, name, shape
+        self.dtype, self.offset, self.nbytes = dtype, offset, nbytes
+
+    def n_elems(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+    def __repr__(self) -> str:
+        return f"TensorInfo({self.name!r}, shape={self.shape}, dtype={self.dtype}, offset={self.offset})"
+
+
+class GgufFile:
+    """GgufFile (swamp-gguf/src/mmap.rs:16-151) over the C reader of
+    include/swamp_gguf.h: the file is mapped read-only; tensor bytes are
+    handed out zero-copy (tensor_raw_bytes) or copied straight to a device
+    buffer (upload).  Errors raise GpuError with the reader's code."""
+
+    def __init__(self, path: str):
+        lib = gpu_lib()
+        h = c_vp()
+        _check(lib.swamp_gguf_open(os.fsencode(path), ctypes.byref(h)), f"swamp_gguf_open({path})")
+        self._h = h
+        self._lib = lib
+        self.version = lib.swamp_gguf_version(h)
+        self.data_offset = lib.swamp_gguf_data_offset(h)
+        self.file_size = lib.swamp_gguf_file_size(h)
+        self.n_kv = lib.swamp_gguf_n_kv(h)
+        self.tensors = [self._info(i) for i in range(lib.swamp_gguf_n_tensors(h))]
+
+    def _info(self, i: int) -> TensorInfo:
+        name = ctypes.c_char_p()
+        dt = ctypes.c_uint32()
+        nd = ctypes.c_int()
+        dims = (ctypes.c_uint64 * 4)()
+        off = ctypes.c_uint64()
+        nb = ctypes.c_uint64()
+        _check(self._lib.swamp_gguf_tensor_info(self._h, i, ctypes.byref(name), ctypes.byref(dt),
+                                                ctypes.byref(nd), dims, ctypes.byref(off),
+                                                ctypes.byref(nb)), "swamp_gguf_tensor_info")
+        shape = [int(dims[d]) for d in range(min(4, nd.value))]
+        return TensorInfo(i, name.value.decode("utf-8", "replace"), shape, dt.value, off.value,
+                          nb.value)
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.swamp_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def n_tensors(self) -> int:
+        return len(self.tensors)
+
+    def tensor(self, name: str) -> Optional[TensorInfo]:
+        i = self._lib.swamp_gguf_find(self._h, name.encode())
+        return self.tensors[i] if i >= 0 else None
+
+    def tensor_or_err(self, name: str) -> TensorInfo:
+        i = self._lib.swamp_gguf_find(self._h, name.encode())
+        _check(int(i) if i < 0 else OK, f"tensor {name!r}")
+        return self.tensors[i]
+
+    def tensor_raw_bytes(self, info: TensorInfo):
+        """numpy uint8 view of the mapping (valid while the file is open)."""
+        np = _np()
+        p, n = c_vp(), c_size()
+        _check(self._lib.swamp_gguf_tensor_raw(self._h, info.index, ctypes.byref(p),
+                                               ctypes.byref(n)), f"tensor_raw_bytes({info.name})")
+        if n.value == 0:
+            return np.zeros(0, np.uint8)
+        buf = (ctypes.c_uint8 * n.value).from_address(p.value)
+        return np.frombuffer(buf, dtype=np.uint8)
+
+    def upload(self, info: TensorInfo, d_dst: int, dst_len: int, stream: int = 0) -> None:
+        _check(self._lib.swamp_gguf_upload(self._h, info.index, d_dst, dst_len, stream),
+               f"upload({info.name})")
+
+    def meta_type(self, key: str) -> Optional[int]:
+        t = ctypes.c_uint32()
+        rc = self._lib.swamp_gguf_meta_type(self._h, key.encode(), ctypes.byref(t))
+        return t.value if rc == OK else None
+
+    def get_u32(self, key: str) -> int:
+        v = ctypes.c_uint32()
+        _check(self._lib.swamp_gguf_meta_u32(self._h, key.encode(), ctypes.byref(v)), key)
+        return v.value
+
+    def get_u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        _check(self._lib.swamp_gguf_meta_u64(self._h, key.encode(), ctypes.byref(v)), key)
+        return v.value
+
+    def get_f32(self, key: str) -> float:
+        v = ctypes.c_float()
+        _check(self._lib.swamp_gguf_meta_f32(self._h, key.encode(), ctypes.byref(v)), key)
+        return v.value
+
+    def get_str(self, key: str) -> str:
+        p, n = ctypes.c_char_p(), c_size()
+        _check(self._lib.swamp_gguf_meta_str(self._h, key.encode(), ctypes.byref(p),
+                                             ctypes.byref(n)), key)
+        return ctypes.string_at(p, n.value).decode("utf-8", "replace")
+
+    def architecture(self) -> str:
+        """Metadata::architecture (metadata.rs:286-290): general.architecture
+        as a string, else "unknown"."""
+        try:
+            return self.get_str("general.architecture")
+        except GpuError:
+            return "unknown"

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "swamp_common.hpp"
+#include "swamp_gguf.h"
 
 namespace swamp {
 
@@ -141,6 +142,11 @@ const char *swamp_strerror(int code) {
   case SWAMP_ELAUNCH: return "HIP launch or copy failed";
   case SWAMP_ENODEVICE: return "no HIP device";
   case SWAMP_EWORKSPACE: return "workspace missing or too small";
+  case SWAMP_EIO: return "GGUF file could not be opened, mapped or fully read";
+  case SWAMP_EMAGIC: return "not a GGUF file (bad magic)";
+  case SWAMP_EVERSION: return "unsupported GGUF version";
+  case SWAMP_ENOTFOUND: return "tensor or metadata key not found";
+  case SWAMP_ETENSOR: return "tensor bytes lie outside the file";
   default: return "unknown error";
   }
 }

@@ -33,6 +33,13 @@ def test_gpu_lib_exports_header(pkg):
     pkg.gpu_lib()  # dlopen + every signature binds
 
 
+def test_gpu_lib_exports_gguf_header(pkg):
+    names = declared("swamp_gguf.h")
+    assert set(names) == set(pkg.GGUF_SYMBOLS)
+    syms = exported(pkg.GPU_LIB_PATH)
+    assert not [n for n in names if n not in syms]
+
+
 def test_quant_lib_exports_header(pkg):
     names = declared("swamp_quant.h")
     assert set(names) == set(pkg.QUANT_SYMBOLS)
@@ -57,7 +64,7 @@ def test_dtype_table_matches_oracle(pkg, orc):
 
 
 def test_strerror(pkg):
-    for code in (0, -1, -2, -3, -4, -5, -6, -77):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11, -77):
         assert isinstance(pkg.strerror(code), str) and pkg.strerror(code)
 
 

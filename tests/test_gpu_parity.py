@@ -455,3 +455,43 @@ def test_legacy_gemv_q8_vnni_kat(pkg, orc, fixtures, torch_dev):
         assert got == float(np.float32(t["dot"]))
         assert L.swamp_gemv_q8_vnni(w.ctypes.data, a.ctypes.data, t["k"], 0.5) == \
             orc.gemv_q8_dot(w, a, 0.5)
+
+
+# ------------------------------------------------------------------ GGUF
+
+def test_gguf_upload_then_gemv(pkg, orc, torch_dev, tmp_path):
+    """The input side of the path end to end: weights written into a GGUF
+    file, read back by the mapped reader (include/swamp_gguf.h), copied to
+    the device by swamp_gguf_upload and multiplied by swamp_qgemv; the
+    oracle multiplies the same bytes taken from the file."""
+    import sys, os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from gguf_writer import STRING, write_gguf
+    torch = torch_dev
+    rows, cols = 700, 4096
+    mats = {"blk.0.attn_q.weight": Q4_0, "blk.0.ffn_down.weight": Q8_0, "output.weight": Q4_K}
+    raws = {n: weights(pkg, dt, rows, cols, mid=60 + i) for i, (n, dt) in enumerate(mats.items())}
+    path = str(tmp_path / "model.gguf")
+    write_gguf(path, [(n, [cols, rows], dt, raws[n].tobytes()) for n, dt in mats.items()],
+               [("general.architecture", STRING, "llama")])
+    x = acts(pkg, 1, cols, mid=61)[0]
+    d_x = up(torch, x)
+    say("gguf upload + gemv", rows, cols)
+    with pkg.GgufFile(path) as g:
+        for name, dt in mats.items():
+            info = g.tensor_or_err(name)
+            assert info.dtype == dt and info.shape == [cols, rows]
+            d_w = torch.zeros(info.nbytes, dtype=torch.uint8, device="cuda")
+            g.upload(info, d_w.data_ptr(), d_w.numel(), stream(torch))
+            with pytest.raises(pkg.GpuError) as e:  # destination too small
+                g.upload(info, d_w.data_ptr(), info.nbytes - 1, stream(torch))
+            assert e.value.code == pkg.ESHAPE
+            host = g.tensor_raw_bytes(info)
+            assert np.array_equal(down(d_w), host)
+            d_y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+            pkg.qgemv(dt, d_w.data_ptr(), d_w.numel(), d_x.data_ptr(), d_y.data_ptr(), info.shape[1],
+                      info.shape[0], stream(torch))
+            torch.cuda.synchronize()
+            ref = orc.forward_linear(dt, host, x, rows, cols, 8)
+            deq = orc.dequantize(dt, host, rows * cols).reshape(rows, cols)
+            assert orc.normalized_error(down(d_y), ref, deq, x) <= TOL

@@ -129,12 +129,13 @@ SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 81
 
 def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
-    (lm_head Q8_0) for 1, 4, 8 and 16 tokens, and the 70B Q4_K layer as
-    batch-1 decode and as a 4096-token bf16 prefill GEMM.  Each matrix is
+    (lm_head Q8_0) for 1, 4, 8 and 16 tokens, the 70B Q4_K layer as
+    batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, and the 70B
+    layer as a 4096-token bf16 prefill GEMM.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU
     sleep; GB/s over the algorithmic bytes, TFLOP/s over 2*M*rows*K."""
     s = stream.cuda_stream
-    bpw = {pkg.Q4_0: 18 / 32, pkg.Q4_K: 144 / 256, pkg.Q8_0: 34 / 32}
+    bpw = {pkg.Q4_0: 18 / 32, pkg.Q4_K: 144 / 256, pkg.Q8_0: 34 / 32, pkg.Q6_K: 210 / 256}
 
     def timed(fn, reps=20):
         for i in range(3):
@@ -189,6 +190,28 @@ def run_sweep(pkg, torch, np, stream, lib):
                               "GB/s": round(tot_b / tot_us / 1e3, 1),
                               "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
                               "matrices": per}), flush=True)
+    # batch-1 decode with every 8B matrix in Q6_K (Q4_K_M files keep lm_head
+    # and part of attn_v / ffn_down in Q6_K)
+    per, tot_b, tot_us = [], 0, 0.0
+    for i, (name, rows, k) in enumerate(SWEEP_8B):
+        dt = pkg.Q6_K
+        copies = max(2, min(8, int(2 * 256e6 // (rows * k * bpw[dt])) + 1))
+        ws = weights_dev(dt, rows, k, SEED ^ 0x700 ^ i, 0.02, copies)
+        x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x800 ^ i, 1.0, 1, k)).cuda()
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        fn = lambda c: check(lib.swamp_qgemv(dt, ws[c % copies].data_ptr(), ws[0].numel(),
+                                             x.data_ptr(), y.data_ptr(), rows, k, s), "swamp_qgemv")
+        us = timed(fn)
+        b = int(rows * k * bpw[dt]) + k * 4 + rows * 4
+        per.append({"name": name, "dtype": "Q6_K", "rows": rows, "k": k, "us": round(us, 2),
+                    "GB/s": round(b / us / 1e3, 1)})
+        tot_b += b
+        tot_us += us
+        del ws, x, y
+    print(json.dumps({"sweep": "llama3-8b decode Q6_K", "n_tok": 1, "alg_bytes": tot_b,
+                      "us": round(tot_us, 1), "GB/s": round(tot_b / tot_us / 1e3, 1),
+                      "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                      "matrices": per}), flush=True)
     # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights
     m = 4096
     per = []

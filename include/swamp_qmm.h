@@ -1,11 +1,11 @@
 /*
  * swamp_qmm.h -- C ABI of libswamp_gpu.so, the MI355X (gfx950) quantized
- * matmul library for GGUF Q4_0 / Q8_0 / Q4_K weights.
+ * matmul library for GGUF Q4_0 / Q8_0 / Q4_K / Q6_K weights.
  *
  * Conventions (all entry points):
  *  - dtype codes are GGML's (swamp-gguf/src/dtype.rs:10-40):
  *      SWAMP_F32 = 0, SWAMP_F16 = 1, SWAMP_Q4_0 = 2, SWAMP_Q8_0 = 8,
- *      SWAMP_Q4_K = 12, SWAMP_BF16 = 30.
+ *      SWAMP_Q4_K = 12, SWAMP_Q6_K = 14, SWAMP_BF16 = 30.
  *  - W is row-major by output row, raw GGUF block bytes exactly as
  *    GgufFile::tensor_raw_bytes returns them (swamp-gguf/src/mmap.rs:110-117):
  *    row r starts at byte r * (n_cols / block) * type_size.
@@ -34,6 +34,7 @@ enum {
   SWAMP_Q4_0 = 2,
   SWAMP_Q8_0 = 8,
   SWAMP_Q4_K = 12,
+  SWAMP_Q6_K = 14,
   SWAMP_BF16 = 30
 };
 

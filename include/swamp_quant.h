@@ -16,6 +16,11 @@
  *         bytes (q4_k.rs:37-53), 128 nibble bytes in "layout A"
  *         (q4_k.rs:290-319): byte 32p+i holds sub-block 2p element i (low)
  *         and sub-block 2p+1 element i (high); value (d*sc)*q - dmin*m.
+ *   Q6_K  210 B / 256 weights: ql[128], qh[64], int8 sc[16], f16 d
+ *         (q6_k.rs:25-28); element 128h + 32k + l (k < 4, l < 32) has its
+ *         low 4 bits in ql[64h + l + 32(k&1)] (low nibble for k < 2, high
+ *         for k >= 2) and bits 4-5 in qh[32h + l] bits 2k..2k+1; value
+ *         (d * sc[e/16]) * (q - 32) for element e (q6_k.rs:36-44).
  *
  * All functions return 0 on success, -1 on a bad argument, -2 on an
  * unsupported dtype.  n_threads <= 0 means "use the hardware threads";
@@ -45,7 +50,7 @@ int swamp_fill_normal(uint64_t seed, float sigma, float *dst, size_t rows,
 
 /* Quantize rows x cols floats (row-major, cols a multiple of the block
  * size) into dtype blocks, row after row.  dtype: 2 = Q4_0, 8 = Q8_0,
- * 12 = Q4_K.  dst holds rows * cols / block * type_size bytes. */
+ * 12 = Q4_K, 14 = Q6_K.  dst holds rows * cols / block * type_size bytes. */
 int swamp_quantize(uint32_t dtype, const float *src, uint8_t *dst, size_t rows,
                    size_t cols, int n_threads);
 

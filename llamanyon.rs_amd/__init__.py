@@ -23,10 +23,11 @@ GPU_LIB_PATH = os.path.join(PKG_DIR, "libswamp_gpu.so")
 QUANT_LIB_PATH = os.path.join(PKG_DIR, "libswamp_quant.so")
 
 # GGML dtype codes (swamp-gguf/src/dtype.rs:10-40)
-F32, F16, Q4_0, Q8_0, Q4_K, BF16 = 0, 1, 2, 8, 12, 30
-DTYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", BF16: "BF16"}
-BLOCK = {Q4_0: 32, Q8_0: 32, Q4_K: 256}
-TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144}
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
+DTYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K",
+               BF16: "BF16"}
+BLOCK = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 
 # return codes (include/swamp_qmm.h, include/swamp_gguf.h)
 OK, EINVAL, EDTYPE, ESHAPE, ELAUNCH, ENODEVICE, EWORKSPACE = 0, -1, -2, -3, -4, -5, -6

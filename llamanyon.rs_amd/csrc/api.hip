@@ -24,7 +24,7 @@ size_t block_size(uint32_t dt) {
   switch (dt) {
   case SWAMP_F32: case SWAMP_F16: case SWAMP_BF16: return 1;
   case SWAMP_Q4_0: case SWAMP_Q8_0: return 32;
-  case SWAMP_Q4_K: return 256;
+  case SWAMP_Q4_K: case SWAMP_Q6_K: return 256;
   default: break;
   }
   // rest of the GgmlDType table (swamp-gguf/src/dtype.rs:79-89)
@@ -52,7 +52,7 @@ size_t type_size(uint32_t dt) {
 }
 
 bool is_weight_dtype(uint32_t dt) {
-  return dt == SWAMP_Q4_0 || dt == SWAMP_Q8_0 || dt == SWAMP_Q4_K;
+  return dt == SWAMP_Q4_0 || dt == SWAMP_Q8_0 || dt == SWAMP_Q4_K || dt == SWAMP_Q6_K;
 }
 
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -203,6 +203,7 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len, const flo
                         void *stream) {
   if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
   if (n_tok < 0) return SWAMP_EINVAL;
+  if (dtype == SWAMP_Q6_K && accumulate) return SWAMP_EDTYPE;  // no Q6_K batched kernel contract
   if (n_tok == 0 || n_rows == 0) return SWAMP_OK;  // linear.rs:184
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (dtype != SWAMP_Q4_K && n_cols % 64 != 0) return SWAMP_ESHAPE;
@@ -217,6 +218,7 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (m < 0) return SWAMP_EINVAL;
   if (x_type != SWAMP_BF16 && x_type != SWAMP_Q8_0) return SWAMP_EDTYPE;
   if (x_type == SWAMP_Q8_0 && dtype == SWAMP_Q4_K) return SWAMP_EDTYPE;
+  if (dtype == SWAMP_Q6_K) return SWAMP_EDTYPE;
   if (m == 0 || n_rows == 0) return SWAMP_OK;
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;

@@ -3,7 +3,8 @@
 // This translation unit is compiled with -ffp-contract=off: the Q4_K value
 // (d*sc)*q - dmin*m must round the product and the difference separately,
 // as the reference's Rust does (swamp-gguf/src/quant/q4_k.rs:296-316).
-// Q4_0 and Q8_0 are one exact-integer-times-scale product each.
+// Q4_0 and Q8_0 are one exact-integer-times-scale product each; Q6_K is
+// (d*sc)*q, two roundings in that order (q6_k.rs:41-44).
 //
 // Work split: one thread writes 8 consecutive outputs, so consecutive
 // threads store consecutive 32-byte runs (coalesced); the few block bytes
@@ -124,6 +125,43 @@ __global__ void dequant_q4_k_kernel(const uint8_t *__restrict__ raw,
   store8<kVec>(dst, base, n, v);
 }
 
+// q6_k::dequant_scalar (q6_k.rs:22-56): the 8 outputs of a thread are
+// elements l0..l0+7 (l0 % 8 == 0) of group j of half h, i.e. outputs
+// 128h + 32j + l.  Their low 4 bits are nibbles of ql[64h + 32(j&1) + l]
+// (low for j < 2, high for j >= 2), bits 4-5 are bits 2j..2j+1 of
+// qh[32h + l], and all 8 share the int8 scale sc[8h + l0/16 + 2j]; value
+// (d * sc) * (q - 32).  Blocks are 210 bytes, so only 2-byte loads.
+template <bool kVec>
+__global__ void dequant_q6_k_kernel(const uint8_t *__restrict__ raw,
+                                    float *__restrict__ dst, size_t n) {
+  const size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t base = g * 8;
+  if (base >= n) return;
+  const size_t b = g >> 5;
+  const int e0 = int(g & 31) * 8;  // first element within the block
+  const int h = e0 >> 7, j = (e0 >> 5) & 3, l0 = e0 & 31;
+  const uint8_t *blk = raw + b * 210;
+  const uint8_t *ql = blk + 64 * h + 32 * (j & 1) + l0;
+  const uint8_t *qh = blk + 128 + 32 * h + l0;
+  const uint32_t l_lo = ld_u16(ql) | (ld_u16(ql + 2) << 16);
+  const uint32_t l_hi = ld_u16(ql + 4) | (ld_u16(ql + 6) << 16);
+  const uint32_t h_lo = ld_u16(qh) | (ld_u16(qh + 2) << 16);
+  const uint32_t h_hi = ld_u16(qh + 4) | (ld_u16(qh + 6) << 16);
+  const int sc = int(int8_t(blk[192 + 8 * h + (l0 >> 4) + 2 * j]));
+  const float d = f16_bits_to_f32_exact(ld_u16(blk + 208));
+  const float ds = d * float(sc);
+  const int nsh = j >= 2 ? 4 : 0;
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const uint32_t lb = ((k < 4 ? l_lo : l_hi) >> (8 * (k & 3))) & 0xFFu;
+    const uint32_t hb = ((k < 4 ? h_lo : h_hi) >> (8 * (k & 3))) & 0xFFu;
+    const int q = int(((lb >> nsh) & 0xFu) | (((hb >> (2 * j)) & 3u) << 4)) - 32;
+    v[k] = ds * float(q);
+  }
+  store8<kVec>(dst, base, n, v);
+}
+
 __global__ void dequant_f16_kernel(const uint16_t *__restrict__ raw,
                                    float *__restrict__ dst, size_t n) {
   const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -162,6 +200,10 @@ int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
   case SWAMP_Q4_K:
     if (vec) dequant_q4_k_kernel<true><<<grid8, threads, 0, s>>>(raw, d_dst, n);
     else dequant_q4_k_kernel<false><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    break;
+  case SWAMP_Q6_K:
+    if (vec) dequant_q6_k_kernel<true><<<grid8, threads, 0, s>>>(raw, d_dst, n);
+    else dequant_q6_k_kernel<false><<<grid8, threads, 0, s>>>(raw, d_dst, n);
     break;
   case SWAMP_F16:
     dequant_f16_kernel<<<grid1, threads, 0, s>>>(static_cast<const uint16_t *>(d_raw), d_dst, n);

@@ -1,10 +1,12 @@
-// gemv.hip -- decode GEMV (one token) for Q4_0 / Q8_0 / Q4_K rows.
+// gemv.hip -- decode GEMV (one token) for Q4_0 / Q8_0 / Q4_K / Q6_K rows.
 //
-// Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and
-// fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:59-82, scalar body
-// :466-508) on the device.
+// Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the
+// kernels it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:
+// 59-82, scalar body :466-508) and fused_gemv_q6k (fused_gemv_q6k.rs:22-41,
+// scalar body :248-291), on the device.
 //
-// Design (HBM-bound; 0.5625 B/weight for Q4_0/Q4_K, 1.0625 for Q8_0):
+// Design (HBM-bound; 0.5625 B/weight for Q4_0/Q4_K, 0.8203 for Q6_K, 1.0625
+// for Q8_0):
 //  * A row is cut into 64-weight "items" (two Q4_0 blocks = 36 B, two Q8_0
 //    blocks = 68 B, a quarter Q4_K super-block = 32 B of nibbles + the 16 B
 //    header).  Lane j of a workgroup always owns item j (+ T, + 2T, ...) of
@@ -18,10 +20,12 @@
 //  * Weights become fp16 pairs with one and-or each: a low nibble q under
 //    the magic 0x6400 is 1024 + q, a high nibble left in place is
 //    1024 + 16 q (its x is pre-divided by 16), an int8 byte flipped to
-//    q + 128 is 1024 + q + 128.  V_DOT2_F32_F16 multiplies a pair by two
-//    fp16 x values exactly and accumulates in fp32; the constant offset is
-//    removed per block with the matching weighted sum of the same fp16 x
-//    values.  Per 8 nibbles: 1 shift + 4 and-or + 4 dot2.
+//    q + 128 is 1024 + q + 128, a 6-bit Q6_K code gets its two qh bits
+//    or-ed in above its nibble (1024 + q, or 1024 + 16 q for high
+//    nibbles).  V_DOT2_F32_F16 multiplies a pair by two fp16 x values
+//    exactly and accumulates in fp32; the constant offset is removed per
+//    block with the matching weighted sum of the same fp16 x values.  Per
+//    8 nibbles: 1 shift + 4 and-or + 4 dot2 (Q6_K: about twice that).
 //  * x is converted to fp16 per item after scaling by a power of two that
 //    puts the item's largest |x| in [2^14, 2^15) (exact; fp16 range safe);
 //    the item's result is scaled back.
@@ -120,13 +124,32 @@ struct XFrag<SWAMP_Q8_0> {
   float c[2];      // per block: 1152 * sum of x
   float scale;
 };
+template <>
+struct XFrag<SWAMP_Q6_K> {
+  uint32_t p[32];  // pair 8t + 2j + e: group j, dword t, bytes (e, e + 2)
+  float c[4];      // per group: the offset sum (1056 x or 1536 x/16)
+  float scale;
+};
 
 // Issue the loads of one item's 64 x values (clamped item: always in
-// bounds; a lane past the row end zeroes its values afterwards).
+// bounds; a lane past the row end zeroes its values afterwards).  A Q6_K
+// item of block b, half h, columns i has x[256b + 128h + 32j + 16i + c] for
+// j < 4, c < 16 in xv[4j + c/4].
+template <int DT>
 __device__ __forceinline__ void load_x(float4 (&xv)[16], const float *__restrict__ x, int item) {
-  const float4 *xp = reinterpret_cast<const float4 *>(x + size_t(item) * 64);
+  if constexpr (DT == SWAMP_Q6_K) {
+    const float *xb = x + size_t(item >> 2) * 256 + 128 * ((item >> 1) & 1) + 16 * (item & 1);
 #pragma unroll
-  for (int i = 0; i < 16; i++) xv[i] = xp[i];
+    for (int j = 0; j < 4; j++) {
+      const float4 *xp = reinterpret_cast<const float4 *>(xb + 32 * j);
+#pragma unroll
+      for (int k = 0; k < 4; k++) xv[4 * j + k] = xp[k];
+    }
+  } else {
+    const float4 *xp = reinterpret_cast<const float4 *>(x + size_t(item) * 64);
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = xp[i];
+  }
 }
 
 template <int DT>
@@ -151,7 +174,29 @@ __device__ __forceinline__ void build_xfrag(XFrag<DT> &xf, const float4 (&x4)[16
   const uint32_t k_lo = 0x64086408u;  // fp16 pair (1032, 1032)
   const uint32_t k_hi = 0x64806480u;  // fp16 pair (1152, 1152)
   const uint32_t k_one = 0x3C003C00u;  // fp16 pair (1, 1)
-  if constexpr (DT == SWAMP_Q8_0) {
+  if constexpr (DT == SWAMP_Q6_K) {
+    // groups j = 0, 1 hold 1024 + q (x scaled by down), groups 2, 3 hold
+    // 1024 + 16 q (x scaled by down/16); sum (q - 32) x = S - c with
+    // c = 1056 sum x (j < 2) or 1536 sum x/16 (j >= 2)
+    const uint32_t k_c01 = 0x64206420u;  // fp16 pair (1056, 1056)
+    const uint32_t k_c23 = 0x66006600u;  // fp16 pair (1536, 1536)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float f = j >= 2 ? down16 : down;
+      float c = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const float *v = xv + 16 * j + 4 * t;
+        const uint32_t p0 = pack_f16(v[0] * f, v[2] * f);
+        const uint32_t p1 = pack_f16(v[1] * f, v[3] * f);
+        xf.p[8 * t + 2 * j] = p0;
+        xf.p[8 * t + 2 * j + 1] = p1;
+        c = dot2(j >= 2 ? k_c23 : k_c01, p0, c);
+        c = dot2(j >= 2 ? k_c23 : k_c01, p1, c);
+      }
+      xf.c[j] = c;
+    }
+  } else if constexpr (DT == SWAMP_Q8_0) {
     float c0 = 0.f, c1 = 0.f;
 #pragma unroll
     for (int t = 0; t < 16; t++)
@@ -229,6 +274,42 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf,
       }
     }
     return (d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1])) * xf.scale;
+  } else if constexpr (DT == SWAMP_Q6_K) {
+    // realign the windows of an odd block by 2 bytes (item bit 2 = block
+    // parity; rows start 4-byte aligned)
+    const uint32_t sh = uint32_t(item & 4) >> 1;
+    const uint32_t ii = uint32_t(item & 1);
+    const uint32_t s01 = __builtin_amdgcn_alignbyte(r.s[1], r.s[0], sh);  // sc[8h .. 8h+3]
+    const uint32_t s23 = __builtin_amdgcn_alignbyte(r.s[2], r.s[1], sh);  // sc[8h+4 .. 8h+7]
+    const float d = swamp::f16_bits_to_f32(__builtin_amdgcn_alignbyte(0u, r.d, sh) & 0xFFFFu);
+    // group j uses sc[8h + i + 2j]: byte i + 2j of s01:s23
+    const float sc0 = float(int(s01 << (24 - 8 * ii)) >> 24);
+    const float sc1 = float(int(s01 << (8 - 8 * ii)) >> 24);
+    const float sc2 = float(int(s23 << (24 - 8 * ii)) >> 24);
+    const float sc3 = float(int(s23 << (8 - 8 * ii)) >> 24);
+    const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, b45 = 0x00300030u, b89 = 0x03000300u;
+    float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t A = __builtin_amdgcn_alignbyte(r.a[t + 1], r.a[t], sh);
+      const uint32_t B = __builtin_amdgcn_alignbyte(r.b[t + 1], r.b[t], sh);
+      const uint32_t H = __builtin_amdgcn_alignbyte(r.h[t + 1], r.h[t], sh);
+      // qh fields moved to bits 4-5 (low-nibble groups) and 8-9 (high-
+      // nibble groups, whose nibble stays at bits 4-7): bytes 0, 2 first
+      const uint32_t hA = H << 4, hB = H >> 4, hC = H << 2, hD = H >> 6;
+      const uint32_t sA = A >> 8, sB = B >> 8;
+      g0 = dot2((A & lo) | (hA & b45) | m, xf.p[8 * t + 0], g0);
+      g0 = dot2((sA & lo) | (hB & b45) | m, xf.p[8 * t + 1], g0);
+      g1 = dot2((B & lo) | (hC & b45) | m, xf.p[8 * t + 2], g1);
+      g1 = dot2((sB & lo) | (hD & b45) | m, xf.p[8 * t + 3], g1);
+      g2 = dot2((A & hi) | (hA & b89) | m, xf.p[8 * t + 4], g2);
+      g2 = dot2((sA & hi) | (hB & b89) | m, xf.p[8 * t + 5], g2);
+      g3 = dot2((B & hi) | (hC & b89) | m, xf.p[8 * t + 6], g3);
+      g3 = dot2((sB & hi) | (hD & b89) | m, xf.p[8 * t + 7], g3);
+    }
+    return d * (sc0 * (g0 - xf.c[0]) + sc1 * (g1 - xf.c[1]) + sc2 * (g2 - xf.c[2]) +
+                sc3 * (g3 - xf.c[3])) *
+           xf.scale;
   } else {
     const float d = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
@@ -409,7 +490,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
   // conversion (which waits for the x loads only).
   float4 x4[kPPT][16];
 #pragma unroll
-  for (int j = 0; j < kPPT; j++) load_x(x4[j], x, item[j]);
+  for (int j = 0; j < kPPT; j++) load_x<DT>(x4[j], x, item[j]);
   Raw<DT> ra[kRows][kPPT], rb[kRows][kPPT];
   TileRef ta = tile_ref<kRows, kMulti>(ms, tile);
   issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
@@ -480,6 +561,52 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(const uint8_t *__rest
   }
 }
 
+// Generic Q6_K path for rows of an odd number of blocks (n_cols % 512 ==
+// 256), whose blocks start at any even byte offset: one wavefront per row,
+// one 16-weight sub-block (one int8 scale) per lane step, byte loads.
+__global__ void __launch_bounds__(256) gemv_generic_q6k_kernel(const uint8_t *__restrict__ w,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y, int n_rows,
+                                                               int n_cols) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nwaves = (gridDim.x * blockDim.x) >> 6;
+  const int nb = n_cols / 256;
+  for (int row = wave; row < n_rows; row += nwaves) {
+    const uint8_t *rp = w + size_t(row) * nb * 210;
+    float acc = 0.f;
+    for (int u = lane; u < nb * 16; u += 64) {
+      const int b = u >> 4, g = u & 15;  // sub-block g: elements 16g .. 16g+15
+      const uint8_t *blk = rp + size_t(b) * 210;
+      const float d = swamp::f16_bits_to_f32(uint32_t(blk[208]) | (uint32_t(blk[209]) << 8));
+      const float sc = float(int8_t(blk[192 + g]));
+      const int h = g >> 3, j = (g >> 1) & 3, l0 = (g & 1) * 16;
+      const float *xg = x + size_t(b) * 256 + 16 * g;
+      float s = 0.f;
+      for (int c = 0; c < 16; c++) {
+        const int l = l0 + c;
+        const uint32_t lb = blk[64 * h + 32 * (j & 1) + l];
+        const uint32_t hb = blk[128 + 32 * h + l];
+        const int q = int(((j >= 2 ? lb >> 4 : lb) & 0xFu) | (((hb >> (2 * j)) & 3u) << 4)) - 32;
+        s += float(q) * xg[c];
+      }
+      acc += d * sc * s;
+    }
+    acc = swamp::wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+  }
+}
+
+// Rows the item kernel takes: whole items, at most 2048 per row, and for
+// Q6_K an even number of blocks (4-byte aligned rows) and at most 1024
+// items (n_cols <= 65536).
+bool item_path_ok(uint32_t dt, int n_cols) {
+  if (n_cols / 64 > 2048) return false;
+  if (dt == SWAMP_Q4_K) return true;
+  if (dt == SWAMP_Q6_K) return n_cols % 512 == 0 && n_cols / 64 <= 1024;
+  return n_cols % 64 == 0;
+}
+
 // Launch shape: waves per CU the persistent grid aims for, and rows per
 // tile (SWAMP_GEMV_WAVES_PER_CU / SWAMP_GEMV_ROWS override them).
 struct Tuning {
@@ -537,16 +664,20 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
 int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
 
 // Rows per tile: 4 when every workgroup of the grid gets at least 8 tiles,
-// else 2 when it gets at least 2, else 1.  Longer tile runs per wave hide
-// the first tile's latency and the x prologue; shorter tiles keep small
-// matrices spread over the whole chip.
+// else 2 when it gets at least 2, else 1; always 1 when a lane holds
+// several items (rows of more than 512 items).  Longer tile runs per wave
+// hide the first tile's latency and the x prologue; shorter tiles keep
+// small matrices spread over the whole chip.
 int tile_rows_for(int n_cols, int total_rows) {
-  if (tuning().rows) return tuning().rows;
+  const int ipr = n_cols / 64;
+  const int cap = ipr <= 512 ? 4 : 1;
+  if (tuning().rows) return std::min(tuning().rows, cap);
   const int cus = swamp::device_info().num_cus;
-  const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(n_cols / 64));
-  if (long(total_rows) / 4 >= 8 * slots) return 4;
-  if (long(total_rows) / 2 >= 2 * slots) return 2;
-  return 1;
+  const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(ipr));
+  int r = 1;
+  if (long(total_rows) / 4 >= 8 * slots) r = 4;
+  else if (long(total_rows) / 2 >= 2 * slots) r = 2;
+  return std::min(r, cap);
 }
 
 template <int DT, int kRows>
@@ -556,8 +687,14 @@ int launch_rows(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
   if (ipr <= 128) return launch_items<DT, 1, kRows, 2>(ms, x, n_cols, s);
   if (ipr <= 256) return launch_items<DT, 1, kRows, 4>(ms, x, n_cols, s);
   if (ipr <= 512) return launch_items<DT, 1, kRows, 8>(ms, x, n_cols, s);
-  if (ipr <= 1024) return launch_items<DT, 2, kRows, 8>(ms, x, n_cols, s);
-  if (ipr <= 2048) return launch_items<DT, 4, kRows, 8>(ms, x, n_cols, s);
+  // With several items per lane the tiles are single rows (tile_rows_for
+  // caps them) so both register buffers fit without spills; a Q6_K item
+  // (19 dwords per row buffer) allows at most two items per lane, longer
+  // Q6_K rows take the generic kernel (item_path_ok).
+  if constexpr (kRows > 1) return SWAMP_ESHAPE;
+  else if (ipr <= 1024) return launch_items<DT, 2, 1, 8>(ms, x, n_cols, s);
+  else if constexpr (DT == SWAMP_Q6_K) return SWAMP_ESHAPE;
+  else if (ipr <= 2048) return launch_items<DT, 4, 1, 8>(ms, x, n_cols, s);
   return SWAMP_ESHAPE;
 }
 
@@ -576,6 +713,7 @@ int dispatch(uint32_t dt, const MatSet &ms, const float *x, int n_cols, int tile
   case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0>(ms, x, n_cols, tile_rows, s);
   case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0>(ms, x, n_cols, tile_rows, s);
   case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K>(ms, x, n_cols, tile_rows, s);
+  case SWAMP_Q6_K: return launch_dt<SWAMP_Q6_K>(ms, x, n_cols, tile_rows, s);
   default: return SWAMP_EDTYPE;
   }
 }
@@ -585,12 +723,14 @@ int dispatch(uint32_t dt, const MatSet &ms, const float *x, int n_cols, int tile
 int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
                       int n_rows, int n_cols, hipStream_t s) {
   if (n_rows == 0) return SWAMP_OK;
-  const bool item_ok = dtype == SWAMP_Q4_K || n_cols % 64 == 0;
-  if (!item_ok || n_cols / 64 > 2048) {
+  if (!item_path_ok(dtype, n_cols)) {
     if (dtype == SWAMP_Q4_K) return SWAMP_ESHAPE;
     const int cus = swamp::device_info().num_cus;
     const int blocks = std::min((n_rows + 3) / 4, cus * 8);
-    if (dtype == SWAMP_Q4_0)
+    if (dtype == SWAMP_Q6_K)
+      gemv_generic_q6k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
+                                                     n_rows, n_cols);
+    else if (dtype == SWAMP_Q4_0)
       gemv_generic_kernel<SWAMP_Q4_0><<<blocks, 256, 0, s>>>(
           static_cast<const uint8_t *>(d_w), d_x, d_y, n_rows, n_cols);
     else
@@ -615,8 +755,7 @@ int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *cons
   for (int i = 0; i < n_mats; i++) {
     if (done[i]) continue;
     const uint32_t dt = dtypes[i];
-    const bool item_ok = dt == SWAMP_Q4_K || (n_cols % 64 == 0 && n_cols / 64 <= 2048);
-    if (!item_ok) {
+    if (!item_path_ok(dt, n_cols)) {
       for (int j = i; j < n_mats; j++)
         if (!done[j] && dtypes[j] == dt) {
           int rc = swamp_launch_gemv(dt, d_ws[j], d_x, d_ys[j], row_counts[j], n_cols, s);

@@ -537,6 +537,17 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
                               int n_tok, int n_rows, int n_cols, int accumulate,
                               hipStream_t s) {
   if (n_rows == 0 || n_tok == 0) return SWAMP_OK;
+  if (dtype == SWAMP_Q6_K) {
+    // forward_linear_batch sends Q6_K to fallback_gemv (linear.rs:336-364):
+    // fused_gemv_q6k per token, written over the output (:357, :361)
+    if (accumulate) return SWAMP_EDTYPE;
+    for (int t = 0; t < n_tok; t++) {
+      const int rc = swamp_launch_gemv(dtype, d_w, d_x + size_t(t) * n_cols,
+                                       d_y + size_t(t) * n_rows, n_rows, n_cols, s);
+      if (rc) return rc;
+    }
+    return SWAMP_OK;
+  }
   Args a{};
   a.w = static_cast<const uint8_t *>(d_w);
   a.n_rows = n_rows;

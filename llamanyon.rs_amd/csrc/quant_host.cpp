@@ -5,7 +5,8 @@
 // ones the reference reads back (see swamp_quant.h).  Q4_0 and Q8_0 use the
 // block formulas ggml publishes for its reference quantizers; Q4_K uses a
 // simple max/min per-sub-block scheme packed with the scale/min bit layout
-// of the reference's test packer (swamp-kernels/src/fused_gemv_q4k.rs:708-724).
+// of the reference's test packer (swamp-kernels/src/fused_gemv_q4k.rs:708-724);
+// Q6_K uses a signed per-sub-block scheme like ggml's (quant_block_q6_k).
 #include "swamp_quant.h"
 
 #include <algorithm>
@@ -159,6 +160,60 @@ void quant_block_q4_k(const float *x, uint8_t *out) {
       out[16 + 32 * p + i] = uint8_t(q[2 * p][i] | (q[2 * p + 1][i] << 4));
 }
 
+// Q6_K: each 16-weight sub-block j gets the signed step s_j = v_j / -32
+// (v_j its value of largest magnitude, so v_j codes as q = 0); the block
+// scale d = s_m / -128 for the s_m of largest magnitude is rounded to f16,
+// sc_j = s_j / d rounded away from zero and clamped to [-128, 127]
+// (negative codes occur), and
+// q = round(x / (d * sc_j)) + 32 clamped to [0, 63].  Packed as the
+// reference's dequantizer reads it (swamp-gguf/src/quant/q6_k.rs:36-44):
+// output 128h + 32k + l (k = 0..3, l < 32) keeps its low 4 bits in byte
+// 64h + l + 32(k & 1) of ql (low nibble for k < 2, high for k >= 2) and
+// its bits 4-5 in bits 2k..2k+1 of qh[32h + l].
+void quant_block_q6_k(const float *x, uint8_t *out) {
+  float s[16];
+  float smax = 0.0f;
+  for (int j = 0; j < 16; j++) {
+    float amax = 0.0f, vmax = 0.0f;
+    for (int i = 0; i < 16; i++) {
+      const float a = std::fabs(x[16 * j + i]);
+      if (amax < a) {
+        amax = a;
+        vmax = x[16 * j + i];
+      }
+    }
+    s[j] = vmax / -32.0f;
+    if (std::fabs(s[j]) > std::fabs(smax)) smax = s[j];
+  }
+  std::memset(out, 0, 210);
+  const uint16_t dh = swamp_f32_to_f16(smax / -128.0f);
+  const float d = f16_to_f32(dh);
+  if (d == 0.0f) return;  // all-zero block: every code 0 decodes to 0
+  int8_t sc[16];
+  for (int j = 0; j < 16; j++) {
+    // magnitude rounded up, so the step covers the sub-block's range
+    const float r = std::copysign(std::ceil(std::fabs(s[j] / d)), s[j] / d);
+    sc[j] = int8_t(std::min(127.0f, std::max(-128.0f, r)));
+  }
+  uint8_t q[256];
+  for (int e = 0; e < 256; e++) {
+    const float step = d * float(sc[e / 16]);
+    const float t = step != 0.0f ? std::round(x[e] / step) : 0.0f;
+    q[e] = uint8_t(std::min(31.0f, std::max(-32.0f, t)) + 32.0f);
+  }
+  for (int h = 0; h < 2; h++)
+    for (int l = 0; l < 32; l++) {
+      const uint8_t *v = q + 128 * h + l;  // v[32k] is output 128h + 32k + l
+      out[64 * h + l] = uint8_t((v[0] & 0xF) | ((v[64] & 0xF) << 4));
+      out[64 * h + l + 32] = uint8_t((v[32] & 0xF) | ((v[96] & 0xF) << 4));
+      out[128 + 32 * h + l] =
+          uint8_t((v[0] >> 4) | ((v[32] >> 4) << 2) | ((v[64] >> 4) << 4) | ((v[96] >> 4) << 6));
+    }
+  for (int j = 0; j < 16; j++) out[192 + j] = uint8_t(sc[j]);
+  out[208] = uint8_t(dh & 0xFF);
+  out[209] = uint8_t(dh >> 8);
+}
+
 struct Fmt {
   size_t block, bytes;
   void (*fn)(const float *, uint8_t *);
@@ -169,6 +224,7 @@ bool fmt_for(uint32_t dtype, Fmt &f) {
   case 2: f = {32, 18, quant_block_q4_0}; return true;
   case 8: f = {32, 34, quant_block_q8_0}; return true;
   case 12: f = {256, 144, quant_block_q4_k}; return true;
+  case 14: f = {256, 210, quant_block_q6_k}; return true;
   default: return false;
   }
 }

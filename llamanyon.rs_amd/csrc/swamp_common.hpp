@@ -13,11 +13,13 @@ namespace swamp {
 constexpr int kQ4_0Block = 32, kQ4_0Bytes = 18;
 constexpr int kQ8_0Block = 32, kQ8_0Bytes = 34;
 constexpr int kQ4_KBlock = 256, kQ4_KBytes = 144;
+constexpr int kQ6_KBlock = 256, kQ6_KBytes = 210;
 
-// One "item" is 64 consecutive weights of one row: two Q4_0 blocks (36 B),
-// two Q8_0 blocks (68 B) or one quarter of a Q4_K super-block (32 nibble
-// bytes plus the block's 16-byte header).  Every kernel that streams rows
-// hands out whole items to lanes.
+// One "item" is 64 weights of one row: two Q4_0 blocks (36 B), two Q8_0
+// blocks (68 B), one quarter of a Q4_K super-block (32 nibble bytes plus
+// the block's 16-byte header) or one quarter of a Q6_K block (48 bytes of
+// ql/qh plus 4 scales and d; its 64 weights are four runs of 16).  Every
+// kernel that streams rows hands out whole items to lanes.
 constexpr int kItem = 64;
 
 __host__ __device__ constexpr int item_bytes(int dt) {
@@ -28,6 +30,7 @@ __host__ __device__ constexpr size_t row_bytes(int dt, size_t n_cols) {
   return dt == SWAMP_Q4_0   ? n_cols / 32 * 18
          : dt == SWAMP_Q8_0 ? n_cols / 32 * 34
          : dt == SWAMP_Q4_K ? n_cols / 256 * 144
+         : dt == SWAMP_Q6_K ? n_cols / 256 * 210
                             : 0;
 }
 

@@ -1,15 +1,31 @@
 // swamp_items.hpp -- raw loads of one 64-weight "item" of a quantized row.
 //
-// An item is two Q4_0 blocks (36 B), two Q8_0 blocks (68 B) or one quarter
-// of a Q4_K super-block (its 16-byte header + 32 nibble bytes).  Rows of
-// n_cols % 64 == 0 (Q4_0/Q8_0) or % 256 == 0 (Q4_K) start at 4-byte (Q4_0,
-// Q8_0) or 16-byte (Q4_K) aligned offsets from an aligned base, so every
-// access below is a dword-aligned vector load.
+// An item is two Q4_0 blocks (36 B), two Q8_0 blocks (68 B), one quarter
+// of a Q4_K super-block (its 16-byte header + 32 nibble bytes) or one
+// quarter of a Q6_K block.  Rows of n_cols % 64 == 0 (Q4_0/Q8_0), % 256 == 0
+// (Q4_K) or % 512 == 0 (Q6_K) start at 4-byte (Q4_0, Q8_0, Q6_K) or 16-byte
+// (Q4_K) aligned offsets from an aligned base, so every access below is a
+// dword-aligned vector load.
 #pragma once
 
 #include "swamp_common.hpp"
 
 namespace swamp {
+
+// A Q6_K block is 210 bytes, so in a row of an even number of blocks (a
+// 4-byte aligned row) the odd blocks start 2 bytes past a dword boundary.
+// A Q6_K item (block b, quarter q: half h = q >> 1, columns i = q & 1)
+// loads dword-aligned windows that start at (field address) & ~3 and are
+// one dword longer than the field; item_dot shifts them by the block's
+// misalignment (0 or 2 bytes, from b's parity).  Fields of the item, as
+// byte offsets in the block:
+//   qlA = 64h + 16i (16 B)   low nibbles: q1, high nibbles: q3
+//   qlB = qlA + 32  (16 B)   low nibbles: q2, high nibbles: q4
+//   qh  = 128 + 32h + 16i (16 B)
+//   sc  = 192 + 8h  (8 B: the item uses sc[8h + i + 2j], j < 4; 12-byte window)
+//   d   = 208 (2 B)
+// Every window lies inside the block, or for an even block inside the
+// next one, which exists because the row has an even number of blocks.
 
 // Raw bytes of one item, loaded with dword-aligned vector loads.
 template <int DT>
@@ -27,6 +43,14 @@ struct Raw<SWAMP_Q4_K> {
   uint32_t h[4];  // d, dmin, 12 scale bytes
   uint32_t q[8];  // 32 nibble bytes of the quarter
 };
+template <>
+struct Raw<SWAMP_Q6_K> {
+  uint32_t a[5];  // qlA window
+  uint32_t b[5];  // qlB window
+  uint32_t h[5];  // qh window
+  uint32_t s[3];  // scale window
+  uint32_t d;     // the dword holding d
+};
 
 // Byte offset of item `item` within its row (32-bit: rows are < 4 GiB), so
 // that loads take the uniform row pointer as a scalar base plus this
@@ -35,12 +59,16 @@ template <int DT>
 __device__ __forceinline__ uint32_t item_offset(int item) {
   if constexpr (DT == SWAMP_Q4_0) return uint32_t(item) * 36u;
   else if constexpr (DT == SWAMP_Q8_0) return uint32_t(item) * 68u;
-  else return uint32_t(item >> 2) * 144u + 16u + 32u * uint32_t(item & 3);
+  else if constexpr (DT == SWAMP_Q4_K) return uint32_t(item >> 2) * 144u + 16u + 32u * uint32_t(item & 3);
+  else  // Q6_K: the aligned start of the item's qlA window
+    return (uint32_t(item >> 2) * 210u & ~3u) + 64u * uint32_t((item >> 1) & 1) +
+           16u * uint32_t(item & 1);
 }
 
 // Raw bytes of the item at byte offset `off` of `row` (from item_offset).
 template <int DT>
 __device__ __forceinline__ void load_raw_at(Raw<DT> &r, const uint8_t *row, uint32_t off, int item) {
+  static_assert(DT != SWAMP_Q6_K, "Q6_K items are loaded through buffer resources");
   if constexpr (DT == SWAMP_Q4_0) {
     const uint8_t *p = row + off;
     u32x4 a = ld4(p), b = ld4(p + 16);
@@ -75,6 +103,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 }
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3v __attribute__((ext_vector_type(3)));
 
 // Raw bytes of one item through a buffer resource: the per-lane item offset
 // in a VGPR (voff) and the per-row offset in an SGPR (soff), so one row
@@ -96,13 +125,30 @@ __device__ __forceinline__ void load_raw_buf(Raw<DT> &r, __amdgpu_buffer_rsrc_t 
       for (int i = 0; i < 4; i++) r.d[4 * j + i] = a[i];
     }
     r.d[16] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 64, soff, 0);
-  } else {
+  } else if constexpr (DT == SWAMP_Q4_K) {
     const uint32_t hoff = voff - 16u - 32u * uint32_t(item & 3);
     const u32x4v h = __builtin_amdgcn_raw_buffer_load_b128(rs, hoff, soff, 0);
     const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
     const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16, soff, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) { r.h[i] = h[i]; r.q[i] = a[i]; r.q[4 + i] = b[i]; }
+  } else {
+    // voff = aligned block start ab + 64h + 16i (item_offset)
+    const uint32_t hh = uint32_t((item >> 1) & 1), ii = uint32_t(item & 1);
+    const uint32_t ab = voff - 64u * hh - 16u * ii;
+    const uint32_t qh = ab + 128u + 32u * hh + 16u * ii;
+    const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    const uint32_t a4 = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 16, soff, 0);
+    const u32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 32, soff, 0);
+    const uint32_t b4 = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 48, soff, 0);
+    const u32x4v h = __builtin_amdgcn_raw_buffer_load_b128(rs, qh, soff, 0);
+    const uint32_t h4 = __builtin_amdgcn_raw_buffer_load_b32(rs, qh + 16, soff, 0);
+    const u32x3v sw = __builtin_amdgcn_raw_buffer_load_b96(rs, ab + 192u + 8u * hh, soff, 0);
+    r.d = __builtin_amdgcn_raw_buffer_load_b32(rs, ab + 208u, soff, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) { r.a[i] = a[i]; r.b[i] = b[i]; r.h[i] = h[i]; }
+    r.a[4] = a4; r.b[4] = b4; r.h[4] = h4;
+    r.s[0] = sw[0]; r.s[1] = sw[1]; r.s[2] = sw[2];
   }
 }
 

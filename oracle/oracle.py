@@ -44,6 +44,8 @@ def lib() -> ctypes.CDLL:
         "or_dequantize": (i32, [u32, c_vp, c_size, c_vp, c_size]),
         "or_unpack_scales_q4k": (None, [c_vp, c_vp, c_vp]),
         "or_fused_gemv_q4k": (i32, [c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size, c_size]),
+        "or_fused_gemv_q6k": (i32, [c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size, c_size]),
+        "or_q6k_f16_raw": (f32, [ctypes.c_uint16]),
         "or_fused_gemv_q4k_batched": (i32, [c_vp, c_vp, c_vp, c_size, c_size, c_size]),
         "or_fused_gemv_q4k_multi": (i32, [c_vp, c_vp, c_vp, c_vp, c_size, c_size]),
         "or_forward_linear": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
@@ -105,6 +107,20 @@ def fused_gemv_q4k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np
     if rc != 0:
         raise ValueError(f"or_fused_gemv_q4k rc={rc}")
     return out
+
+
+def fused_gemv_q6k(w: np.ndarray, x: np.ndarray, n_rows: int, n_cols: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(n_rows, dtype=np.float32)
+    rc = lib().or_fused_gemv_q6k(_p(w), w.size, _p(x), x.size, _p(out), out.size, n_rows, n_cols)
+    if rc != 0:
+        raise ValueError(f"or_fused_gemv_q6k rc={rc}")
+    return out
+
+
+def q6k_f16_raw(code: int) -> float:
+    return float(lib().or_q6k_f16_raw(code))
 
 
 def fused_gemv_q4k_batched(w: np.ndarray, xs: np.ndarray, outs: np.ndarray, n_rows: int,

@@ -212,6 +212,46 @@ int or_dequant_q4_k(const uint8_t *raw, size_t raw_len, float *dst, size_t n) {
   return 0;
 }
 
+/* q6_k::dequant_q6k, swamp-gguf/src/quant/q6_k.rs:7-56.  A 256-weight
+ * block is 210 bytes: ql[128], qh[64], int8 sc[16], f16 d (:25-28).  Two
+ * halves of 128 outputs; in a half, l < 32 gives outputs l, l+32, l+64,
+ * l+96 from the low nibble of ql[l], the low nibble of ql[l+32], the high
+ * nibble of ql[l], the high nibble of ql[l+32], each with the next 2-bit
+ * field of qh[l] as bits 4-5 (:36-39); value (d * sc[l/16 + 2j]) * (q - 32)
+ * (:41-44), then ql += 64, qh += 32, sc += 8 (:47-49).  The last block may
+ * be partial (:52-54). */
+int or_dequant_q6_k(const uint8_t *raw, size_t raw_len, float *dst, size_t n) {
+  size_t n_blocks = (n + 255) / 256;
+  if (raw_len < n_blocks * 210) return -1; /* BufferTooSmall, :11-16 */
+  for (size_t b = 0; b < n_blocks; b++) {
+    const uint8_t *ql = raw + b * 210;
+    const uint8_t *qh = ql + 128;
+    const int8_t *sc = (const int8_t *)(ql + 192);
+    float d = f16_le(ql + 208);
+    float y[256];
+    for (int h = 0; h < 2; h++) {
+      for (int l = 0; l < 32; l++) {
+        int is = l / 16;
+        int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+        int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+        y[128 * h + l] = d * (float)sc[is] * (float)q1;
+        y[128 * h + l + 32] = d * (float)sc[is + 2] * (float)q2;
+        y[128 * h + l + 64] = d * (float)sc[is + 4] * (float)q3;
+        y[128 * h + l + 96] = d * (float)sc[is + 6] * (float)q4;
+      }
+      ql += 64;
+      qh += 32;
+      sc += 8;
+    }
+    size_t start = b * 256;
+    size_t count = n - start < 256 ? n - start : 256;
+    memcpy(dst + start, y, count * sizeof(float));
+  }
+  return 0;
+}
+
 /* swamp-gguf/src/quant/mod.rs:18-33 (+ dequant_f32 :35-44, f16.rs:6-28) */
 int or_dequantize(uint32_t dtype, const uint8_t *raw, size_t raw_len,
                   float *dst, size_t n) {
@@ -232,6 +272,7 @@ int or_dequantize(uint32_t dtype, const uint8_t *raw, size_t raw_len,
   case 2: return or_dequant_q4_0(raw, raw_len, dst, n);
   case 8: return or_dequant_q8_0(raw, raw_len, dst, n);
   case 12: return or_dequant_q4_k(raw, raw_len, dst, n);
+  case 14: return or_dequant_q6_k(raw, raw_len, dst, n);
   default: return -2; /* other dtypes are off this path */
   }
 }
@@ -336,11 +377,82 @@ int or_fused_gemv_q4k_multi(const uint8_t *const *raws, const float *x,
 }
 
 /* ---------------------------------------------------------------------- */
+/* Q6_K fused GEMV (scalar)                                                */
+/* ---------------------------------------------------------------------- */
+
+/* f16_to_f32_raw, swamp-kernels/src/fused_gemv_q6k.rs:11-21: the fused Q6_K
+ * kernels' private decode of d.  It equals or_f16_to_f32 for exponent
+ * fields 1..30.  Exponent 0 (zero and subnormal codes) gives
+ * sign | ((1023 - 14) << 23 wrapped to 32 bits = 0xF8800000) | man << 13, a
+ * negative value near -2^114; exponent 31 (inf, NaN) decodes as the finite
+ * 2^16 * (1 + man/1024). */
+float or_q6k_f16_raw(uint16_t v) {
+  uint32_t sign = (uint32_t)(v >> 15) << 31;
+  uint32_t exp = (v >> 10) & 0x1Fu;
+  uint32_t man = v & 0x3FFu;
+  if (exp == 0) return bits_f32(sign | (1009u << 23) | (man << 13));
+  return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* One Q6_K block against 256 x values in the order of the scalar kernel,
+ * fused_gemv_q6k.rs:253-286: half 0..1, l = 0..31, then the four terms
+ * ((d * sc) * q) * x[l + 32j] for j = 0..3, each added to acc.  Scales are
+ * int8 (:277-280).  d is decoded exactly (half::f16, as the dequantizer
+ * q6_k.rs:28 does), not with f16_to_f32_raw: the two agree on every code
+ * with exponent field 1..30. */
+static float q6k_block_dot(const uint8_t *base, const float *x_blk, float acc) {
+  float d = f16_le(base + 208);
+  const uint8_t *ql = base, *qh = base + 128;
+  const int8_t *sc = (const int8_t *)(base + 192);
+  for (int h = 0; h < 2; h++) {
+    const uint8_t *ql_h = ql + 64 * h, *qh_h = qh + 32 * h;
+    const int8_t *sc_h = sc + 8 * h;
+    const float *xh = x_blk + 128 * h;
+    for (int l = 0; l < 32; l++) {
+      int is = l / 16;
+      float q1 = (float)((int)((ql_h[l] & 0x0F) | ((qh_h[l] & 3) << 4)) - 32);
+      float q2 = (float)((int)((ql_h[l + 32] & 0x0F) | (((qh_h[l] >> 2) & 3) << 4)) - 32);
+      float q3 = (float)((int)((ql_h[l] >> 4) | (((qh_h[l] >> 4) & 3) << 4)) - 32);
+      float q4 = (float)((int)((ql_h[l + 32] >> 4) | (((qh_h[l] >> 6) & 3) << 4)) - 32);
+      acc = acc + d * (float)sc_h[is] * q1 * xh[l];
+      acc = acc + d * (float)sc_h[is + 2] * q2 * xh[l + 32];
+      acc = acc + d * (float)sc_h[is + 4] * q3 * xh[l + 64];
+      acc = acc + d * (float)sc_h[is + 6] * q4 * xh[l + 96];
+    }
+  }
+  return acc;
+}
+
+/* fused_gemv_q6k_scalar, fused_gemv_q6k.rs:248-291 (one f32 accumulator per
+ * row, block after block; overwrites out[row]). */
+static void q6k_scalar(const uint8_t *w, const float *x, float *out,
+                       size_t n_rows, size_t n_blocks) {
+  for (size_t row = 0; row < n_rows; row++) {
+    float acc = 0.0f;
+    for (size_t blk = 0; blk < n_blocks; blk++)
+      acc = q6k_block_dot(w + (row * n_blocks + blk) * 210, x + blk * 256, acc);
+    out[row] = acc;
+  }
+}
+
+int or_fused_gemv_q6k(const uint8_t *w_raw, size_t w_len, const float *x,
+                      size_t x_len, float *out, size_t out_len, size_t n_rows,
+                      size_t n_cols) {
+  if (n_cols % 256 != 0) return -1;
+  size_t nb = n_cols / 256;
+  if (w_len < n_rows * nb * 210) return -1;
+  if (x_len < n_cols) return -1;
+  if (out_len < n_rows) return -1;
+  q6k_scalar(w_raw, x, out, n_rows, nb);
+  return 0;
+}
+
+/* ---------------------------------------------------------------------- */
 /* forward_linear and friends (row-partitioned worker threads)             */
 /* ---------------------------------------------------------------------- */
 
 typedef struct {
-  int kind; /* 0 = Q4_K fused, 1 = dense f32 dot over deq */
+  int kind; /* 0 = Q4_K fused, 1 = dense f32 dot over deq, 2 = Q6_K fused */
   const uint8_t *raw;
   const float *deq;
   const float *x;
@@ -354,6 +466,9 @@ static void run_slice(const slice_job *j) {
   if (j->kind == 0) {
     size_t nb = j->nc / 256;
     q4k_scalar(j->raw + j->rs * nb * 144, j->x, j->out + j->rs, rc, nb);
+  } else if (j->kind == 2) {
+    size_t nb = j->nc / 256;
+    q6k_scalar(j->raw + j->rs * nb * 210, j->x, j->out + j->rs, rc, nb);
   } else {
     /* linear.rs:81-85: s += deq[i*nc+j] * x[j], sequential f32 */
     for (size_t i = 0; i < rc; i++) {
@@ -418,7 +533,13 @@ int or_forward_linear(uint32_t dtype, const uint8_t *raw, size_t raw_len,
     proto.kind = 0;
     return run_partitioned(proto, nr, n_threads);
   }
-  if (dtype == 14) return -2; /* Q6_K arm: off this path */
+  if (dtype == 14) { /* Q6_K arm, :48-66 */
+    /* the reference takes nc / 256 blocks without a check; a row that is
+     * not whole blocks is rejected here */
+    if (nc % 256 != 0) return -1;
+    proto.kind = 2;
+    return run_partitioned(proto, nr, n_threads);
+  }
   /* `_` arm, :68-88: whole-tensor dequant on the calling thread first */
   float *deq = (float *)calloc(nr * nc ? nr * nc : 1, sizeof(float));
   if (!deq) return -3;

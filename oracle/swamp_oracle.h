@@ -51,6 +51,8 @@ int or_dequantize(uint32_t dtype, const uint8_t *raw, size_t raw_len,
 int or_dequant_q4_0(const uint8_t *raw, size_t raw_len, float *dst, size_t n);
 int or_dequant_q8_0(const uint8_t *raw, size_t raw_len, float *dst, size_t n);
 int or_dequant_q4_k(const uint8_t *raw, size_t raw_len, float *dst, size_t n);
+/* q6_k::dequant_q6k, swamp-gguf/src/quant/q6_k.rs:7-56 */
+int or_dequant_q6_k(const uint8_t *raw, size_t raw_len, float *dst, size_t n);
 
 /* unpack_scales, q4_k.rs:37-53 == unpack_scales_q4k fused_gemv_q4k.rs:30-43 */
 void or_unpack_scales_q4k(const uint8_t sc[12], uint8_t scales[8],
@@ -61,6 +63,17 @@ void or_unpack_scales_q4k(const uint8_t sc[12], uint8_t scales[8],
 int or_fused_gemv_q4k(const uint8_t *w_raw, size_t w_len, const float *x,
                       size_t x_len, float *out, size_t out_len, size_t n_rows,
                       size_t n_cols);
+
+/* fused_gemv_q6k with the scalar body, swamp-kernels/src/fused_gemv_q6k.rs:
+ * 248-291 (int8 scales, sequential f32 accumulation, overwrites out), d
+ * decoded exactly like the dequantizer (q6_k.rs:28).  The reference's own
+ * decode of d, f16_to_f32_raw (:11-21), is restated as or_q6k_f16_raw; it
+ * agrees on every code with exponent field 1..30 and mis-decodes zero,
+ * subnormal, inf and NaN codes.  n_cols % 256 != 0 -> -1. */
+int or_fused_gemv_q6k(const uint8_t *w_raw, size_t w_len, const float *x,
+                      size_t x_len, float *out, size_t out_len, size_t n_rows,
+                      size_t n_cols);
+float or_q6k_f16_raw(uint16_t v);
 
 /* fused_gemv_q4k_batched with the scalar body, :527-554 + :650-698.
  * Loop order block -> row -> token; ACCUMULATES into out (out[t][row] +=). */
@@ -78,7 +91,8 @@ int or_fused_gemv_q4k_multi(const uint8_t *const *raws, const float *x,
  * this path -> allocate nr*nc f32, dequantize the whole tensor on one
  * thread, then per row a sequential f32 dot (:68-88).  n_threads worker
  * threads partition rows exactly like the rayon closure; the result does
- * not depend on n_threads.  Q6_K (:48-66) is out of this path: -2. */
+ * not depend on n_threads.  Q6_K -> row slices through or_fused_gemv_q6k
+ * (:48-66; n_cols % 256 != 0 -> -1). */
 int or_forward_linear(uint32_t dtype, const uint8_t *raw, size_t raw_len,
                       const float *x, size_t x_len, float *out, size_t out_len,
                       size_t n_rows, size_t n_cols, int n_threads);
@@ -87,7 +101,9 @@ int or_forward_linear(uint32_t dtype, const uint8_t *raw, size_t raw_len,
  * row slices through the batched scalar kernel.  Other dtypes: the
  * reference's fallback_gemv (:336-364) decodes non-Q4_K bytes as Q4_K
  * (:358), which is a bug; this restatement applies forward_linear per token
- * instead (the semantics the engine's decode path gives each token).
+ * instead (the semantics the engine's decode path gives each token).  For
+ * Q6_K that is exactly fallback_gemv's Q6_K arm (:357): fused_gemv_q6k per
+ * token, written over the output.
  * xs is [bs][n_cols] contiguous, outs is [bs][n_rows] contiguous. */
 int or_forward_linear_batch(uint32_t dtype, const uint8_t *raw, size_t raw_len,
                             const float *xs, float *outs, size_t bs,

@@ -8,7 +8,11 @@ vectors come from:
     expected values from closed forms evaluated in float64 / exact integers;
   * hand-written known answers for the block layouts the reference's scalar
     dequantizers read (q4_0.rs:30-35 interleaved nibbles; q4_k.rs:290-319
-    layout A), written out literally below.
+    layout A), written out literally below;
+  * a Q6_K block built by a packer written from the published layout (the
+    inverse direction of q6_k.rs:36-44), and the reference's Q6_K GEMV test
+    data create_test_data (fused_gemv_q6k.rs:329-357) with its values read
+    back through the same layout.
 Run:  python tests/golden/make_fixtures.py
 """
 import json
@@ -92,6 +96,88 @@ def int8_dot_kat():
     return trials
 
 
+# ------------------------------------------------------------------ Q6_K
+# Layout of a 210-byte Q6_K block as ggml publishes it and the reference's
+# dequantizer reads it (swamp-gguf/src/quant/q6_k.rs:25-49): ql[128],
+# qh[64], int8 sc[16], f16 d.  Element e (0..255) is in half h = e // 128,
+# group k = (e % 128) // 32, column l = e % 32; its 6-bit code q has the low
+# 4 bits in ql[64h + 32(k & 1) + l] (low nibble for k < 2, high for k >= 2)
+# and bits 4-5 in qh[32h + l] bits 2k..2k+1; its scale is sc[e // 16]; its
+# value is d * sc * (q - 32).
+
+def q6k_pack(q, sc, d_code):
+    """Block bytes for codes q[256] (0..63), int8 scales sc[16], f16 d."""
+    b = [0] * 210
+    for e, v in enumerate(q):
+        h, k, l = e // 128, (e % 128) // 32, e % 32
+        i = 64 * h + 32 * (k & 1) + l
+        b[i] |= (v & 0xF) << (4 if k >= 2 else 0)
+        b[128 + 32 * h + l] |= ((v >> 4) & 3) << (2 * k)
+    for j in range(16):
+        b[192 + j] = sc[j] & 0xFF
+    b[208], b[209] = d_code & 0xFF, d_code >> 8
+    return b
+
+
+def q6k_codes(blk):
+    """Inverse of q6k_pack: (q[256], sc[16], d_code) of a block."""
+    q = []
+    for e in range(256):
+        h, k, l = e // 128, (e % 128) // 32, e % 32
+        lo = blk[64 * h + 32 * (k & 1) + l]
+        lo = (lo >> 4) if k >= 2 else (lo & 0xF)
+        q.append(lo | (((blk[128 + 32 * h + l] >> (2 * k)) & 3) << 4))
+    sc = [v - 256 if v >= 128 else v for v in blk[192:208]]
+    return q, sc, blk[208] | (blk[209] << 8)
+
+
+def q6k_create_test_data(n_rows, n_blocks):
+    # the reference's fixture, fused_gemv_q6k.rs:329-357
+    raw = []
+    for row in range(n_rows):
+        for _ in range(n_blocks):
+            b = [0] * 210
+            for i in range(128):
+                b[i] = (i & 0x0F) | (((i + 128) & 0x0F) << 4)
+            for i in range(64):
+                b0 = (i >> 4) & 3
+                b1 = ((i + 64) >> 4) & 3
+                b2 = ((i + 128) >> 4) & 3
+                b3 = ((i + 192) >> 4) & 3
+                b[128 + i] = b0 | (b1 << 2) | (b2 << 4) | (b3 << 6)
+            for i in range(16):
+                b[192 + i] = (row * 16 + i + 1) & 0x7F
+            b[208], b[209] = 0x00, 0x38  # d = 0.5
+            raw += b
+    return raw
+
+
+def q6k_fixtures():
+    out = {}
+    # layout KAT: distinct codes, signed scales (-128 included), d = 1
+    q = [(7 * e + 3) % 64 for e in range(256)]
+    sc = [1, -2, 3, -4, 5, -6, 7, -8, 9, -10, 11, -12, 13, -14, 15, -128]
+    blk = q6k_pack(q, sc, 0x3C00)
+    assert q6k_codes(blk) == (q, sc, 0x3C00)
+    out["q6_k_layout_kat"] = {"raw": blk, "q": q, "sc": sc,
+                              "expected": [float(sc[e // 16] * (q[e] - 32)) for e in range(256)]}
+    # the reference's GEMV test data, with its per-element values from the
+    # layout above (exact: d = 0.5, small integers)
+    fxs = []
+    for n_rows, n_blocks in ((2, 2), (4, 3)):
+        raw = q6k_create_test_data(n_rows, n_blocks)
+        vals = []
+        for r in range(n_rows):
+            for b in range(n_blocks):
+                off = (r * n_blocks + b) * 210
+                qq, ss, dc = q6k_codes(raw[off:off + 210])
+                assert dc == 0x3800
+                vals += [0.5 * ss[e // 16] * (qq[e] - 32) for e in range(256)]
+        fxs.append({"n_rows": n_rows, "n_blocks": n_blocks, "raw": raw, "w_values": vals})
+    out["q6_k_reference_test_data"] = fxs
+    return out
+
+
 def main():
     fx = {}
     # Q4_0 interleave KAT (q4_0.rs:30-35): element 2j is the LOW nibble of
@@ -132,6 +218,7 @@ def main():
         w, x, y, wv = gemv_closed_form(n_rows)
         fx["gemv_fixtures"].append({"n_rows": n_rows, "w": w, "x": x, "y": y, "w_value": wv})
     fx["int8_dot_kat"] = int8_dot_kat()
+    fx.update(q6k_fixtures())
     with open(os.path.join(HERE, "fixtures.json"), "w") as f:
         json.dump(fx, f)
     print("wrote", os.path.join(HERE, "fixtures.json"))

@@ -18,6 +18,7 @@ ENTRIES = [
     (12, 0x5EED ^ (3 << 32) ^ 1, 0.02, 16, 4096),
     (8, 0x5EED ^ (3 << 32) ^ 4, 0.02, 16, 4096),
     (12, 0x5EED ^ (5 << 32) ^ 2, 0.015, 4, 8192),
+    (14, 0x5EED ^ (7 << 32) ^ 5, 0.02, 16, 4096),
 ]
 
 

@@ -71,8 +71,8 @@ def test_strerror(pkg):
 def test_argument_validation_precedes_device(pkg):
     L = pkg.gpu_lib()
     fake = 0x10000  # never dereferenced: every call below fails validation
-    # unsupported dtype (Q6_K = 14)
-    assert L.swamp_qgemv(14, fake, 1 << 20, fake, fake, 4, 256, None) == pkg.EDTYPE
+    # unsupported dtype (Q5_K = 13)
+    assert L.swamp_qgemv(13, fake, 1 << 20, fake, fake, 4, 256, None) == pkg.EDTYPE
     # n_cols not a multiple of the block
     assert L.swamp_qgemv(pkg.Q4_K, fake, 1 << 20, fake, fake, 4, 255, None) == pkg.ESHAPE
     assert L.swamp_qgemv(pkg.Q4_0, fake, 1 << 20, fake, fake, 4, 48, None) == pkg.ESHAPE
@@ -85,7 +85,15 @@ def test_argument_validation_precedes_device(pkg):
     assert L.swamp_qgemv_batched(pkg.Q4_0, fake, 1 << 20, fake, fake, -1, 4, 64, 0, None) == pkg.EINVAL
     assert L.swamp_qgemm(pkg.Q4_K, fake, 1 << 20, fake, pkg.Q8_0, fake, 4, 4, 256, None) == pkg.EDTYPE
     assert L.swamp_qgemm(pkg.Q4_0, fake, 1 << 20, fake, pkg.F16, fake, 4, 4, 64, None) == pkg.EDTYPE
-    assert L.swamp_qdequant(14, fake, 1 << 20, fake, 64, None) == pkg.EDTYPE
+    assert L.swamp_qdequant(13, fake, 1 << 20, fake, 64, None) == pkg.EDTYPE
+    # Q6_K: whole 256-blocks, 4-byte aligned rows base, enough bytes; no
+    # accumulating batched form and no GEMM
+    assert L.swamp_qgemv(pkg.Q6_K, fake, 1 << 20, fake, fake, 4, 300, None) == pkg.ESHAPE
+    assert L.swamp_qgemv(pkg.Q6_K, fake, 4 * 420 - 1, fake, fake, 4, 512, None) == pkg.ESHAPE
+    assert L.swamp_qgemv(pkg.Q6_K, fake + 2, 1 << 20, fake, fake, 4, 512, None) == pkg.EINVAL
+    assert L.swamp_qgemv_batched(pkg.Q6_K, fake, 1 << 20, fake, fake, 2, 4, 512, 1, None) == pkg.EDTYPE
+    assert L.swamp_qgemm(pkg.Q6_K, fake, 1 << 20, fake, pkg.BF16, fake, 4, 4, 512, None) == pkg.EDTYPE
+    assert L.swamp_qdequant(pkg.Q6_K, fake, 419, fake, 512, None) == pkg.ESHAPE
     assert L.swamp_qdequant(pkg.Q4_0, fake, 35, fake, 64, None) == pkg.ESHAPE
     assert L.swamp_quantize_q8_0(fake, pkg.F32, fake, 33, None) == pkg.ESHAPE
     n = 9

@@ -73,7 +73,7 @@ def test_roundtrip_bound_q4_k(pkg, orc):
 
 
 def test_synth_equals_fill_then_quantize(pkg):
-    for dt in (Q4_0, Q8_0, Q4_K):
+    for dt in (Q4_0, Q8_0, Q4_K, 14):
         a = pkg.synth_quantized(dt, 77, 0.02, 16, 512, n_threads=3)
         b = pkg.quantize(dt, pkg.fill_normal(77, 0.02, 16, 512))
         assert np.array_equal(a, b)
@@ -84,7 +84,8 @@ def test_quantize_rejects_bad_shapes(pkg):
     src = np.zeros((2, 48), dtype=np.float32)
     dst = np.zeros(1024, dtype=np.uint8)
     assert L.swamp_quantize(Q4_0, src.ctypes.data, dst.ctypes.data, 2, 48, 1) == -1
-    assert L.swamp_quantize(14, src.ctypes.data, dst.ctypes.data, 2, 64, 1) == -2
+    assert L.swamp_quantize(13, src.ctypes.data, dst.ctypes.data, 2, 64, 1) == -2  # Q5_K
+    assert L.swamp_quantize(14, src.ctypes.data, dst.ctypes.data, 2, 64, 1) == -1  # Q6_K: cols % 256
 
 
 def test_generator_fixture_hashes(pkg):

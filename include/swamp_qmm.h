@@ -64,8 +64,8 @@ size_t swamp_type_size(uint32_t dtype);
 size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
 
 /* quant::dequantize (swamp-gguf/src/quant/mod.rs:18-33) on the device, for
- * F32, F16, BF16, Q4_0 (q4_0.rs:11-39), Q8_0 (q8_0.rs:15-40) and Q4_K
- * (q4_k.rs:21-33, 278-321).  Writes n floats to d_dst, bit-identical to the
+ * F32, F16, BF16, Q4_0 (q4_0.rs:11-39), Q8_0 (q8_0.rs:15-40), Q4_K
+ * (q4_k.rs:21-33, 278-321) and Q6_K (q6_k.rs:7-56; d_raw 2-byte aligned).  Writes n floats to d_dst, bit-identical to the
  * reference's scalar CPU dequantizer (NaN inputs give NaN outputs).
  * raw_len < nbytes_for(dtype, n) -> SWAMP_ESHAPE (the reference's
  * BufferTooSmall, q4_0.rs:15-20). */
@@ -73,10 +73,18 @@ int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
                    float *d_dst, size_t n, void *stream);
 
 /* Decode GEMV, y = W x, OVERWRITING y[0..n_rows).
- * Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the kernel
- * it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:59-82).
- * dtype Q4_0, Q8_0 or Q4_K; n_cols a multiple of the block size (32, or 256
- * for Q4_K); w_len >= nbytes_for(dtype, n_rows * n_cols). */
+ * Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the
+ * kernels it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:
+ * 59-82) and fused_gemv_q6k (fused_gemv_q6k.rs:22-41).
+ * dtype Q4_0, Q8_0, Q4_K or Q6_K; n_cols a multiple of the block size (32,
+ * or 256 for Q4_K and Q6_K); w_len >= nbytes_for(dtype, n_rows * n_cols);
+ * d_w 4-byte aligned (16 for Q4_K), d_x 16-byte aligned.  n_cols == 0
+ * gives y = 0.
+ * Q6_K follows the dequantizer's arithmetic (int8 scales, exact f16 d,
+ * q6_k.rs:28-44), as the reference's scalar GEMV does for every d whose
+ * exponent field is 1..30; the reference's private f16 decode
+ * (fused_gemv_q6k.rs:11-21) mis-decodes zero and subnormal d, and its SIMD
+ * arms read the int8 scales as unsigned (:71-74, :164-167). */
 int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
                 const float *d_x, float *d_y, int n_rows, int n_cols,
                 void *stream);
@@ -92,6 +100,33 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
                       const int *row_counts, const float *d_x,
                       float *const *d_ys, int n_cols, void *stream);
 
+/* RMSNorm fused into the GEMV's x prologue: y_m = W_m x_norm with
+ * x_norm = (x * inv_rms) * norm_w, inv_rms = 1 / sqrt(sum(x^2) / n_cols +
+ * eps), each y_m OVERWRITTEN; x_norm is not written.  Replaces the
+ * engine's rmsnorm (swamp-engine/src/ops.rs:188-201) followed by
+ * forward_linear_multi / forward_linear on its output (executor.rs:433-445
+ * QKV, :488-499 gate+up, :523-526 logits).  Arguments as swamp_qgemv_multi
+ * plus d_norm_w (n_cols floats, 16-byte aligned) and eps.  The sum of
+ * squares is reduced in a different order than the reference's sequential
+ * loop.  n_cols <= 32768 and a whole number of 64-weight items (multiple of
+ * 64; 256 for Q4_K; 512 for Q6_K), else SWAMP_ESHAPE. */
+int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes,
+                        const void *const *d_ws, const size_t *w_lens,
+                        const int *row_counts, const float *d_x,
+                        const float *d_norm_w, float eps, float *const *d_ys,
+                        int n_cols, void *stream);
+
+/* SiLU(gate) * up fused into the GEMV's x prologue (the FFN down
+ * projection): h = gate / (1 + exp(-gate)) * up, then y = W h
+ * (accumulate = 0) or y += W h (accumulate = 1, the residual add).
+ * Replaces silu + mul_in_place (swamp-engine/src/ops.rs:203-214) +
+ * forward_linear + add_in_place (:216-220) at executor.rs:501-505.
+ * d_gate, d_up: n_cols floats each, 16-byte aligned.  Shape rules as
+ * swamp_qgemv_rmsnorm. */
+int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
+                       const float *d_gate, const float *d_up, float *d_y,
+                       int n_rows, int n_cols, int accumulate, void *stream);
+
 /* Small-batch GEMV/GEMM for speculative verify and continuous batching:
  * n_tok tokens, d_x is [n_tok][n_cols] fp32, d_y is [n_tok][n_rows] fp32.
  * accumulate = 0: y = W x (forward_linear_batch zeroes its outputs first,
@@ -99,7 +134,10 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
  * fused_gemv_q4k_batched, fused_gemv_q4k.rs:527-554, :694).
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
- * 16 tokens. */
+ * 16 tokens (Q4_0, Q8_0, Q4_K).  Q6_K: forward_linear_batch sends it to
+ * fallback_gemv (linear.rs:336-364), the GEMV per token written over y;
+ * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
+ * SWAMP_EDTYPE. */
 int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
                         const float *d_x, float *d_y, int n_tok, int n_rows,
                         int n_cols, int accumulate, void *stream);
@@ -115,8 +153,8 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     32-weight block) against W's int8 codes (Q4_0: nibble - 8), each
  *     block's int32 result scaled by d_w * d_x into fp32.  Q4_0 and Q8_0
  *     weights only; n_cols a multiple of 128.
- * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only); bf16 x needs n_cols a
- * multiple of 64.  No workspace: when the tiles do not fill the GPU, K is
+ * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only; Q6_K -> SWAMP_EDTYPE);
+ * bf16 x needs n_cols a multiple of 64.  No workspace: when the tiles do not fill the GPU, K is
  * split across workgroups that add into y (zeroed by a fill kernel first). */
 int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,

@@ -38,6 +38,7 @@ MULTI_MAX = 8
 GPU_SYMBOLS = (
     "swamp_gpu_init", "swamp_strerror", "swamp_block_size", "swamp_type_size",
     "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_multi",
+    "swamp_qgemv_rmsnorm", "swamp_qgemv_swiglu",
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_quantize_q8_0",
     "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
 )
@@ -98,6 +99,10 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_qgemv_multi": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
                                     ctypes.POINTER(c_size), ctypes.POINTER(i32), c_vp,
                                     ctypes.POINTER(c_vp), i32, c_vp]),
+        "swamp_qgemv_rmsnorm": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
+                                      ctypes.POINTER(c_size), ctypes.POINTER(i32), c_vp, c_vp,
+                                      ctypes.c_float, ctypes.POINTER(c_vp), i32, c_vp]),
+        "swamp_qgemv_swiglu": (i32, [u32, c_vp, c_size, c_vp, c_vp, c_vp, i32, i32, i32, c_vp]),
         "swamp_qgemv_batched": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, i32, i32, c_vp]),
         "swamp_qgemm": (i32, [u32, c_vp, c_size, c_vp, u32, c_vp, i32, i32, i32, c_vp]),
         "swamp_quantize_q8_0": (i32, [c_vp, u32, c_vp, c_size, c_vp]),
@@ -202,6 +207,25 @@ def qgemv_multi(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int
     ys = (c_vp * n)(*d_ys)
     _check(gpu_lib().swamp_qgemv_multi(n, u32s, ws, lens, rows, d_x, ys, n_cols, stream),
            "swamp_qgemv_multi")
+
+
+def qgemv_rmsnorm(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int],
+                  row_counts: Sequence[int], d_x: int, d_norm_w: int, eps: float,
+                  d_ys: Sequence[int], n_cols: int, stream: int = 0) -> None:
+    n = len(dtypes)
+    u32s = (ctypes.c_uint32 * n)(*dtypes)
+    ws = (c_vp * n)(*d_ws)
+    lens = (c_size * n)(*w_lens)
+    rows = (ctypes.c_int * n)(*row_counts)
+    ys = (c_vp * n)(*d_ys)
+    _check(gpu_lib().swamp_qgemv_rmsnorm(n, u32s, ws, lens, rows, d_x, d_norm_w, eps, ys, n_cols,
+                                         stream), "swamp_qgemv_rmsnorm")
+
+
+def qgemv_swiglu(dtype: int, d_w: int, w_len: int, d_gate: int, d_up: int, d_y: int,
+                 n_rows: int, n_cols: int, accumulate: bool = False, stream: int = 0) -> None:
+    _check(gpu_lib().swamp_qgemv_swiglu(dtype, d_w, w_len, d_gate, d_up, d_y, n_rows, n_cols,
+                                        1 if accumulate else 0, stream), "swamp_qgemv_swiglu")
 
 
 def qgemv_batched(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_tok: int,

@@ -1,11 +1,12 @@
 // api.hip -- the C ABI of libswamp_gpu.so (declared in include/swamp_qmm.h).
 //
 // Validation and dispatch only; kernels live in dequant.hip, gemv.hip,
-// gemv_batched.hip and gemm.hip.  The error behaviour mirrors the
+// gemv_fused.hip, gemv_batched.hip, gemm.hip and gemm_i8.hip.  The error behaviour mirrors the
 // reference: shape asserts of fused_gemv_q4k (fused_gemv_q4k.rs:66-70) and
 // the bail! of forward_linear (linear.rs:23-25) become negative return
 // codes, checked before anything is launched; the two legacy host-pointer
 // exports keep their silent-return behaviour.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -86,6 +87,14 @@ int check_gemv_args(uint32_t dtype, const void *d_w, size_t w_len, int n_rows, i
   return SWAMP_OK;
 }
 
+// Rows the fused-prologue GEMVs take: the item kernel with one item per
+// lane (whole 64-weight items, Q6_K rows of an even number of blocks,
+// n_cols <= 32768).
+bool fused_cols_ok(uint32_t dt, int n_cols) {
+  if (n_cols <= 0 || n_cols > 32768) return false;
+  return n_cols % (dt == SWAMP_Q6_K ? 512 : dt == SWAMP_Q4_K ? 256 : 64) == 0;
+}
+
 }  // namespace
 
 const DeviceInfo &device_info() {
@@ -115,6 +124,21 @@ __global__ void i8dot_kernel(const int8_t *__restrict__ w, const int8_t *__restr
 }
 
 }  // namespace
+
+// y[0..n) = 0 for a sum over no columns (n_cols == 0), with a kernel so the
+// call stays capturable in a graph.
+static __global__ void fill_zero_kernel(float *__restrict__ y, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += size_t(gridDim.x) * blockDim.x)
+    y[i] = 0.0f;
+}
+
+static int fill_zero(float *d_y, size_t n, hipStream_t s) {
+  if (n == 0) return SWAMP_OK;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  fill_zero_kernel<<<unsigned(blocks), 256, 0, s>>>(d_y, n);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
 
 int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k, int *d_out, hipStream_t s) {
   i8dot_kernel<<<1, 256, 0, s>>>(d_w, d_a, k, d_out);
@@ -179,6 +203,7 @@ int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x,
   if (!aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_rows == 0) return SWAMP_OK;
   if (int rc = ensure_device(nullptr)) return rc;
+  if (n_cols == 0) return fill_zero(d_y, size_t(n_rows), static_cast<hipStream_t>(stream));
   return swamp_launch_gemv(dtype, d_w, d_x, d_y, n_rows, n_cols, static_cast<hipStream_t>(stream));
 }
 
@@ -194,8 +219,46 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_w
     if (!d_ys[i] || !aligned(d_ys[i], 4)) return SWAMP_EINVAL;
   }
   if (int rc = ensure_device(nullptr)) return rc;
+  if (n_cols == 0) {
+    for (int i = 0; i < n_mats; i++)
+      if (int rc = fill_zero(d_ys[i], size_t(row_counts[i]), static_cast<hipStream_t>(stream)))
+        return rc;
+    return SWAMP_OK;
+  }
   return swamp_launch_gemv_multi(n_mats, dtypes, d_ws, row_counts, d_x, d_ys, n_cols,
                                  static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
+                        const size_t *w_lens, const int *row_counts, const float *d_x,
+                        const float *d_norm_w, float eps, float *const *d_ys, int n_cols,
+                        void *stream) {
+  if (n_mats < 0 || n_mats > SWAMP_MULTI_MAX) return SWAMP_EINVAL;
+  if (n_mats == 0) return SWAMP_OK;
+  if (!dtypes || !d_ws || !w_lens || !row_counts || !d_ys || !d_x || !d_norm_w)
+    return SWAMP_EINVAL;
+  if (!aligned(d_x, 16) || !aligned(d_norm_w, 16)) return SWAMP_EINVAL;
+  for (int i = 0; i < n_mats; i++) {
+    if (int rc = check_gemv_args(dtypes[i], d_ws[i], w_lens[i], row_counts[i], n_cols)) return rc;
+    if (!fused_cols_ok(dtypes[i], n_cols)) return SWAMP_ESHAPE;
+    if (!d_ys[i] || !aligned(d_ys[i], 4)) return SWAMP_EINVAL;
+  }
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemv_rmsnorm(n_mats, dtypes, d_ws, row_counts, d_x, d_norm_w, eps, d_ys,
+                                   n_cols, static_cast<hipStream_t>(stream));
+}
+
+int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len, const float *d_gate,
+                       const float *d_up, float *d_y, int n_rows, int n_cols, int accumulate,
+                       void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (!fused_cols_ok(dtype, n_cols)) return SWAMP_ESHAPE;
+  if (!d_gate || !d_up || !d_y) return SWAMP_EINVAL;
+  if (!aligned(d_gate, 16) || !aligned(d_up, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (n_rows == 0) return SWAMP_OK;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_gemv_swiglu(dtype, d_w, d_gate, d_up, d_y, n_rows, n_cols,
+                                  accumulate ? 1 : 0, static_cast<hipStream_t>(stream));
 }
 
 int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x,
@@ -208,6 +271,10 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len, const flo
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (dtype != SWAMP_Q4_K && n_cols % 64 != 0) return SWAMP_ESHAPE;
   if (int rc = ensure_device(nullptr)) return rc;
+  if (n_cols == 0)
+    return accumulate ? SWAMP_OK
+                      : fill_zero(d_y, size_t(n_tok) * size_t(n_rows),
+                                  static_cast<hipStream_t>(stream));
   return swamp_launch_gemv_batched(dtype, d_w, d_x, d_y, n_tok, n_rows, n_cols, accumulate ? 1 : 0,
                                    static_cast<hipStream_t>(stream));
 }
@@ -223,6 +290,8 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;
   if (int rc = ensure_device(nullptr)) return rc;
+  if (n_cols == 0)
+    return fill_zero(d_y, size_t(m) * size_t(n_rows), static_cast<hipStream_t>(stream));
   return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols,
                            static_cast<hipStream_t>(stream));
 }

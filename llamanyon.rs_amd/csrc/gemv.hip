@@ -33,496 +33,11 @@
 //    transposed butterfly (cross-half exchanges first, each halving the
 //    number of live values, then DPP adds), then over the waves of the
 //    workgroup through LDS.
-#include "swamp_common.hpp"
-#include "swamp_items.hpp"
-
-#include <algorithm>
-#include <cstdlib>
+#include "gemv_core.hpp"
 
 namespace {
 
 using swamp::Raw;
-using swamp::load_raw;
-using swamp::q4k_scales;
-using swamp::shr16;
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c,
-                                false);
-}
-
-// Two floats -> packed fp16 pair, round to nearest even (V_CVT_PK_F16_F32).
-__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
-  half2_t v;
-  v[0] = (_Float16)lo;
-  v[1] = (_Float16)hi;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// fp16 pair (1024, 1024) in a VGPR the compiler cannot see through, so that
-// (w & mask) | magic selects V_AND_OR_B32 with the mask in an SGPR (gfx9
-// VOP3 encodings take no literal).
-__device__ __forceinline__ uint32_t f16_magic() {
-  uint32_t m;
-  asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
-  return m;
-}
-
-// Four fp16 pairs of one nibble dword w:
-//   P0 = lo(b0), lo(b2)   P1 = lo(b1), lo(b3)     (value 1024 + q)
-//   P2 = hi(b0), hi(b2)   P3 = hi(b1), hi(b3)     (value 1024 + 16 q)
-__device__ __forceinline__ void nib_pairs(uint32_t w, uint32_t m, uint32_t (&P)[4]) {
-  const uint32_t s = w >> 8;
-  P[0] = (w & 0x000F000Fu) | m;
-  P[1] = (s & 0x000F000Fu) | m;
-  P[2] = (w & 0x00F000F0u) | m;
-  P[3] = (s & 0x00F000F0u) | m;
-}
-
-// Element (0..63 within the item) that half h of pair p of nibble dword t
-// multiplies.  Nibble n of dword t (n = 0..7, bit offset 4n) is:
-//   Q4_0: byte n/2 of the dword, element 8t' + 2(n/2) + (n%2) of block t/4
-//         (interleaved layout, q4_0.rs:30-35), t' = t%4;
-//   Q4_K: low nibble of byte b -> sub-block A element 4t+b,
-//         high nibble -> sub-block B (item elements 32..63) element 4t+b.
-// Pairs p = 2, 3 hold high nibbles (their x is divided by 16).
-template <int DT>
-__host__ __device__ constexpr int nib_elem(int t, int p, int h) {
-  const int byte = (p & 1) + 2 * h;  // P0: b0,b2  P1: b1,b3  P2: b0,b2  P3: b1,b3
-  const int high = p >= 2;
-  if (DT == SWAMP_Q4_0) return 32 * (t / 4) + 8 * (t % 4) + 2 * byte + high;
-  return 32 * high + 4 * t + byte;  // Q4_K
-}
-
-// Element of half h of pair j (0, 1) of int8 dword t of a Q8_0 item (after
-// the block-0 bytes are realigned): bytes j and j + 2.
-__host__ __device__ constexpr int q8_elem(int t, int j, int h) { return 4 * t + j + 2 * h; }
-
-// Per-lane x fragment for one item: fp16 pairs in the order the weight
-// pairs are formed, the offset corrections, and the item's scale 2^e.
-template <int DT>
-struct XFrag;
-
-template <>
-struct XFrag<SWAMP_Q4_0> {
-  uint32_t p[32];  // 8 nibble dwords x 4 pairs
-  float c[2];      // per block: sum of 1032 x (low) + 1152 x/16 (high)
-  float scale;
-};
-template <>
-struct XFrag<SWAMP_Q4_K> {
-  uint32_t p[32];
-  float sa;    // sum of x over sub-block A (low nibbles)
-  float sb16;  // sum of x/16 over sub-block B (high nibbles)
-  float scale;
-};
-template <>
-struct XFrag<SWAMP_Q8_0> {
-  uint32_t p[32];  // 16 int8 dwords x 2 pairs
-  float c[2];      // per block: 1152 * sum of x
-  float scale;
-};
-template <>
-struct XFrag<SWAMP_Q6_K> {
-  uint32_t p[32];  // pair 8t + 2j + e: group j, dword t, bytes (e, e + 2)
-  float c[4];      // per group: the offset sum (1056 x or 1536 x/16)
-  float scale;
-};
-
-// Issue the loads of one item's 64 x values (clamped item: always in
-// bounds; a lane past the row end zeroes its values afterwards).  A Q6_K
-// item of block b, half h, columns i has x[256b + 128h + 32j + 16i + c] for
-// j < 4, c < 16 in xv[4j + c/4].
-template <int DT>
-__device__ __forceinline__ void load_x(float4 (&xv)[16], const float *__restrict__ x, int item) {
-  if constexpr (DT == SWAMP_Q6_K) {
-    const float *xb = x + size_t(item >> 2) * 256 + 128 * ((item >> 1) & 1) + 16 * (item & 1);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float4 *xp = reinterpret_cast<const float4 *>(xb + 32 * j);
-#pragma unroll
-      for (int k = 0; k < 4; k++) xv[4 * j + k] = xp[k];
-    }
-  } else {
-    const float4 *xp = reinterpret_cast<const float4 *>(x + size_t(item) * 64);
-#pragma unroll
-    for (int i = 0; i < 16; i++) xv[i] = xp[i];
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ void build_xfrag(XFrag<DT> &xf, const float4 (&x4)[16], bool valid) {
-  float xv[64];
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    xv[4 * i] = x4[i].x; xv[4 * i + 1] = x4[i].y; xv[4 * i + 2] = x4[i].z; xv[4 * i + 3] = x4[i].w;
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; i++) {
-    xv[i] = valid ? xv[i] : 0.f;
-    amax = fmaxf(amax, fabsf(xv[i]));
-  }
-  // scale 2^(141 - E) maps amax (biased exponent E) into [2^14, 2^15)
-  int E = int((__float_as_uint(amax) >> 23) & 0xFFu);
-  E = E < 15 ? 15 : E > 254 ? 254 : E;
-  const float down = __uint_as_float(uint32_t(268 - E) << 23);
-  xf.scale = __uint_as_float(uint32_t(E - 14) << 23);
-  const float down16 = down * 0.0625f;
-  const uint32_t k_lo = 0x64086408u;  // fp16 pair (1032, 1032)
-  const uint32_t k_hi = 0x64806480u;  // fp16 pair (1152, 1152)
-  const uint32_t k_one = 0x3C003C00u;  // fp16 pair (1, 1)
-  if constexpr (DT == SWAMP_Q6_K) {
-    // groups j = 0, 1 hold 1024 + q (x scaled by down), groups 2, 3 hold
-    // 1024 + 16 q (x scaled by down/16); sum (q - 32) x = S - c with
-    // c = 1056 sum x (j < 2) or 1536 sum x/16 (j >= 2)
-    const uint32_t k_c01 = 0x64206420u;  // fp16 pair (1056, 1056)
-    const uint32_t k_c23 = 0x66006600u;  // fp16 pair (1536, 1536)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float f = j >= 2 ? down16 : down;
-      float c = 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const float *v = xv + 16 * j + 4 * t;
-        const uint32_t p0 = pack_f16(v[0] * f, v[2] * f);
-        const uint32_t p1 = pack_f16(v[1] * f, v[3] * f);
-        xf.p[8 * t + 2 * j] = p0;
-        xf.p[8 * t + 2 * j + 1] = p1;
-        c = dot2(j >= 2 ? k_c23 : k_c01, p0, c);
-        c = dot2(j >= 2 ? k_c23 : k_c01, p1, c);
-      }
-      xf.c[j] = c;
-    }
-  } else if constexpr (DT == SWAMP_Q8_0) {
-    float c0 = 0.f, c1 = 0.f;
-#pragma unroll
-    for (int t = 0; t < 16; t++)
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const uint32_t pr = pack_f16(xv[q8_elem(t, j, 0)] * down, xv[q8_elem(t, j, 1)] * down);
-        xf.p[2 * t + j] = pr;
-        if (t < 8) c0 = dot2(k_hi, pr, c0);
-        else c1 = dot2(k_hi, pr, c1);
-      }
-    xf.c[0] = c0;
-    xf.c[1] = c1;
-  } else {
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; t++)
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const float f = p >= 2 ? down16 : down;
-        const uint32_t pr = pack_f16(xv[nib_elem<DT>(t, p, 0)] * f, xv[nib_elem<DT>(t, p, 1)] * f);
-        xf.p[4 * t + p] = pr;
-        if constexpr (DT == SWAMP_Q4_0) {
-          // both halves of a pair lie in block t / 4
-          if (t < 4) s0 = dot2(p >= 2 ? k_hi : k_lo, pr, s0);
-          else s1 = dot2(p >= 2 ? k_hi : k_lo, pr, s1);
-        } else {
-          if (p < 2) s0 = dot2(k_one, pr, s0);
-          else s1 = dot2(k_one, pr, s1);
-        }
-      }
-    if constexpr (DT == SWAMP_Q4_0) {
-      xf.c[0] = s0;
-      xf.c[1] = s1;
-    } else {
-      xf.sa = s0;
-      xf.sb16 = s1;
-    }
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf, int item,
-                                          uint32_t m) {
-  if constexpr (DT == SWAMP_Q4_0) {
-    const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
-    const float d1 = swamp::f16_bits_to_f32(r.d[4] >> 16);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const uint32_t w = t < 4 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1];
-      uint32_t P[4];
-      nib_pairs(w, m, P);
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        if (t < 4) s0 = dot2(P[p], xf.p[4 * t + p], s0);
-        else s1 = dot2(P[p], xf.p[4 * t + p], s1);
-      }
-    }
-    return (d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1])) * xf.scale;
-  } else if constexpr (DT == SWAMP_Q8_0) {
-    const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
-    const float d1 = swamp::f16_bits_to_f32(r.d[8] >> 16);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int t = 0; t < 16; t++) {
-      const uint32_t w = (t < 8 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1]) ^ 0x80808080u;
-      const uint32_t P0 = (w & 0x00FF00FFu) | m;
-      const uint32_t P1 = ((w >> 8) & 0x00FF00FFu) | m;
-      if (t < 8) {
-        s0 = dot2(P0, xf.p[2 * t], s0);
-        s0 = dot2(P1, xf.p[2 * t + 1], s0);
-      } else {
-        s1 = dot2(P0, xf.p[2 * t], s1);
-        s1 = dot2(P1, xf.p[2 * t + 1], s1);
-      }
-    }
-    return (d0 * (s0 - xf.c[0]) + d1 * (s1 - xf.c[1])) * xf.scale;
-  } else if constexpr (DT == SWAMP_Q6_K) {
-    // realign the windows of an odd block by 2 bytes (item bit 2 = block
-    // parity; rows start 4-byte aligned)
-    const uint32_t sh = uint32_t(item & 4) >> 1;
-    const uint32_t ii = uint32_t(item & 1);
-    const uint32_t s01 = __builtin_amdgcn_alignbyte(r.s[1], r.s[0], sh);  // sc[8h .. 8h+3]
-    const uint32_t s23 = __builtin_amdgcn_alignbyte(r.s[2], r.s[1], sh);  // sc[8h+4 .. 8h+7]
-    const float d = swamp::f16_bits_to_f32(__builtin_amdgcn_alignbyte(0u, r.d, sh) & 0xFFFFu);
-    // group j uses sc[8h + i + 2j]: byte i + 2j of s01:s23
-    const float sc0 = float(int(s01 << (24 - 8 * ii)) >> 24);
-    const float sc1 = float(int(s01 << (8 - 8 * ii)) >> 24);
-    const float sc2 = float(int(s23 << (24 - 8 * ii)) >> 24);
-    const float sc3 = float(int(s23 << (8 - 8 * ii)) >> 24);
-    const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, b45 = 0x00300030u, b89 = 0x03000300u;
-    float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const uint32_t A = __builtin_amdgcn_alignbyte(r.a[t + 1], r.a[t], sh);
-      const uint32_t B = __builtin_amdgcn_alignbyte(r.b[t + 1], r.b[t], sh);
-      const uint32_t H = __builtin_amdgcn_alignbyte(r.h[t + 1], r.h[t], sh);
-      // qh fields moved to bits 4-5 (low-nibble groups) and 8-9 (high-
-      // nibble groups, whose nibble stays at bits 4-7): bytes 0, 2 first
-      const uint32_t hA = H << 4, hB = H >> 4, hC = H << 2, hD = H >> 6;
-      const uint32_t sA = A >> 8, sB = B >> 8;
-      g0 = dot2((A & lo) | (hA & b45) | m, xf.p[8 * t + 0], g0);
-      g0 = dot2((sA & lo) | (hB & b45) | m, xf.p[8 * t + 1], g0);
-      g1 = dot2((B & lo) | (hC & b45) | m, xf.p[8 * t + 2], g1);
-      g1 = dot2((sB & lo) | (hD & b45) | m, xf.p[8 * t + 3], g1);
-      g2 = dot2((A & hi) | (hA & b89) | m, xf.p[8 * t + 4], g2);
-      g2 = dot2((sA & hi) | (hB & b89) | m, xf.p[8 * t + 5], g2);
-      g3 = dot2((B & hi) | (hC & b89) | m, xf.p[8 * t + 6], g3);
-      g3 = dot2((sB & hi) | (hD & b89) | m, xf.p[8 * t + 7], g3);
-    }
-    return d * (sc0 * (g0 - xf.c[0]) + sc1 * (g1 - xf.c[1]) + sc2 * (g2 - xf.c[2]) +
-                sc3 * (g3 - xf.c[3])) *
-           xf.scale;
-  } else {
-    const float d = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
-    const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
-    uint32_t sc0, m0, sc1, m1;
-    q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
-    float sa = 0.f, sb = 0.f;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      uint32_t P[4];
-      nib_pairs(r.q[t], m, P);
-      sa = dot2(P[0], xf.p[4 * t + 0], sa);
-      sa = dot2(P[1], xf.p[4 * t + 1], sa);
-      sb = dot2(P[2], xf.p[4 * t + 2], sb);
-      sb = dot2(P[3], xf.p[4 * t + 3], sb);
-    }
-    // sum (d*sc*q - dmin*m) x = d*sc*(S - 1024 Sx) - dmin*m*Sx, with B's x
-    // carried as x/16
-    const float qa = sa - 1024.0f * xf.sa, qb = sb - 1024.0f * xf.sb16;
-    return (d * (float(sc0) * qa + float(sc1) * qb) -
-            dmin * (float(m0) * xf.sa + float(m1) * 16.0f * xf.sb16)) *
-           xf.scale;
-  }
-}
-
-// ---- wavefront reduction of kRows partial sums ---------------------------
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
-}
-
-// One transposed butterfly level on lane bit `off`: lanes with the bit clear
-// keep values [0, n/2), lanes with it set keep [n/2, n); each lane adds the
-// partner's copy of the values it keeps.
-template <int N>
-__device__ __forceinline__ void tr_level(float (&v)[N], int n, int off, int lane) {
-  const bool up = (lane & off) != 0;
-#pragma unroll
-  for (int i = 0; i < N / 2; i++) {
-    if (i < n / 2) {
-      const float send = up ? v[i] : v[i + n / 2];
-      const float keep = up ? v[i + n / 2] : v[i];
-      v[i] = keep + __shfl_xor(send, off, 64);
-    }
-  }
-}
-
-// After reduce_rows<R>, lane l holds the wavefront total of row
-// l >> (6 - log2 R) in v[0].  The xor masks used (32, 16, 15 = row mirror,
-// 7 = half-row mirror, 2, 1) are linearly independent over GF(2), so every
-// lane's partial is counted exactly once; masks after a transposed level
-// never flip that level's bit.
-template <int R>
-__device__ __forceinline__ void reduce_rows(float (&v)[R], int lane) {
-  static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per tile");
-  if constexpr (R >= 2) tr_level<R>(v, R, 32, lane);
-  else v[0] += __shfl_xor(v[0], 32, 64);
-  if constexpr (R >= 4) tr_level<R>(v, R / 2, 16, lane);
-  else v[0] += __shfl_xor(v[0], 16, 64);
-  if constexpr (R >= 8) {
-    // bit 3 through the row mirror (lane ^ 15): its bits 0..2 flips are
-    // harmless because the later levels reduce over those bits anyway.
-    const bool up = (lane & 8) != 0;
-    const float send = up ? v[0] : v[1];
-    const float keep = up ? v[1] : v[0];
-    v[0] = keep + dpp<0x140>(send);
-  } else {
-    v[0] += dpp<0x140>(v[0]);  // row mirror
-  }
-  v[0] += dpp<0x141>(v[0]);  // half-row mirror (lane ^ 7)
-  v[0] += dpp<0x4E>(v[0]);   // quad_perm [2,3,0,1]
-  v[0] += dpp<0xB1>(v[0]);   // quad_perm [1,0,3,2]
-}
-
-constexpr int kMaxMats = SWAMP_MULTI_MAX;
-
-struct MatSet {
-  const uint8_t *w[kMaxMats];
-  float *y[kMaxMats];
-  int rows[kMaxMats];
-  int tile_end[kMaxMats];  // cumulative tile counts
-  int n;
-};
-
-struct TileRef {
-  const uint8_t *w;
-  float *y;
-  int row0, nrows;
-};
-
-template <int kRows, bool kMulti>
-__device__ __forceinline__ TileRef tile_ref(const MatSet &ms, int tile) {
-  if constexpr (!kMulti) return TileRef{ms.w[0], ms.y[0], tile * kRows, ms.rows[0]};
-  int m = 0;
-  while (m + 1 < ms.n && tile >= ms.tile_end[m]) m++;
-  const int first = m ? ms.tile_end[m - 1] : 0;
-  return TileRef{ms.w[m], ms.y[m], (tile - first) * kRows, ms.rows[m]};
-}
-
-// One buffer descriptor per tile (base = the tile's first row); row r of
-// the tile is the scalar offset r * row_bytes (rows past the matrix end
-// are clamped to its last row, so every load stays in bounds).
-template <int DT, int kPPT, int kRows>
-__device__ __forceinline__ void issue_tile(Raw<DT> (&raw)[kRows][kPPT], const TileRef &t,
-                                           size_t row_bytes, const int (&item)[kPPT],
-                                           const uint32_t (&off)[kPPT]) {
-  const uint32_t rb = uint32_t(row_bytes);
-  const __amdgpu_buffer_rsrc_t rs =
-      swamp::make_rsrc(t.w + size_t(t.row0) * row_bytes, rb * kRows);
-#pragma unroll
-  for (int r = 0; r < kRows; r++) {
-    const int rr = min(t.row0 + r, t.nrows - 1) - t.row0;
-#pragma unroll
-    for (int j = 0; j < kPPT; j++)
-      swamp::load_raw_buf<DT>(raw[r][j], rs, off[j], uint32_t(rr) * rb, item[j]);
-  }
-}
-
-template <int DT, int kPPT, int kRows, int kWaves>
-__device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
-                                             const XFrag<DT> (&xf)[kPPT], const TileRef &t,
-                                             const int (&item)[kPPT],
-                                             float (*red)[kRows], int tid, uint32_t m) {
-  const int lane = tid & 63, wave = tid >> 6;
-  float acc[kRows];
-#pragma unroll
-  for (int r = 0; r < kRows; r++) {
-    acc[r] = 0.f;
-#pragma unroll
-    for (int j = 0; j < kPPT; j++) acc[r] += item_dot<DT>(raw[r][j], xf[j], item[j], m);
-  }
-  reduce_rows<kRows>(acc, lane);
-  constexpr int kGroup = 64 / kRows;  // lanes holding one row's total
-  const int rr = lane / kGroup;
-  if constexpr (kWaves == 1) {
-    if (lane % kGroup == 0 && t.row0 + rr < t.nrows) t.y[t.row0 + rr] = acc[0];
-  } else {
-    if (lane % kGroup == 0) red[wave][rr] = acc[0];
-    __syncthreads();
-    if (tid < kRows && t.row0 + tid < t.nrows) {
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; w++) v += red[w][tid];
-      t.y[t.row0 + tid] = v;
-    }
-  }
-}
-
-// One workgroup = 64 * kWaves lanes; lane j owns items j, j + T, ...
-// (kPPT items per lane), covering one row of ipr items.  The workgroup
-// walks tiles blockIdx.x, + gridDim.x, ... of kRows rows each.
-template <int DT, int kPPT, int kRows, int kWaves, bool kMulti>
-__global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const float *__restrict__ x,
-                                                           int ipr, size_t row_bytes,
-                                                           int n_tiles) {
-  constexpr int T = 64 * kWaves;
-  __shared__ float red[2][kWaves][kRows];
-  const int tid = threadIdx.x;
-
-  int item[kPPT];
-  bool valid[kPPT];
-#pragma unroll
-  for (int j = 0; j < kPPT; j++) {
-    const int it = tid + j * T;
-    valid[j] = it < ipr;
-    item[j] = valid[j] ? it : ipr - 1;  // in-bounds stand-in; its x is zero
-  }
-  uint32_t off[kPPT];
-#pragma unroll
-  for (int j = 0; j < kPPT; j++) off[j] = swamp::item_offset<DT>(item[j]);
-
-  int tile = blockIdx.x;
-  if (tile >= n_tiles) return;
-  const uint32_t m = f16_magic();
-
-  // x loads first, then the first tile's weight loads, then the x
-  // conversion (which waits for the x loads only).
-  float4 x4[kPPT][16];
-#pragma unroll
-  for (int j = 0; j < kPPT; j++) load_x<DT>(x4[j], x, item[j]);
-  Raw<DT> ra[kRows][kPPT], rb[kRows][kPPT];
-  TileRef ta = tile_ref<kRows, kMulti>(ms, tile);
-  issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
-  // keep every load of the tile ahead of the arithmetic (the scheduler would
-  // otherwise sink them into registers freed by the current tile)
-  __builtin_amdgcn_sched_barrier(0);
-  XFrag<DT> xf[kPPT];
-#pragma unroll
-  for (int j = 0; j < kPPT; j++) build_xfrag<DT>(xf[j], x4[j], valid[j]);
-
-  // Two tiles per trip so both register buffers have static names.  The
-  // next tile's loads are issued unconditionally (past the last tile they
-  // re-read the current one, already in cache), so every path through the
-  // loop has the same number of loads in flight and the hardware wait
-  // counts stay tight.
-  for (;;) {
-    int nxt = tile + gridDim.x;
-    const TileRef tb = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
-    issue_tile<DT, kPPT, kRows>(rb, tb, row_bytes, item, off);
-    __builtin_amdgcn_sched_barrier(0);
-    consume_tile<DT, kPPT, kRows, kWaves>(ra, xf, ta, item, red[0], tid, m);
-    if (nxt >= n_tiles) break;
-    tile = nxt;
-    nxt = tile + gridDim.x;
-    ta = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
-    issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
-    __builtin_amdgcn_sched_barrier(0);
-    consume_tile<DT, kPPT, kRows, kWaves>(rb, xf, tb, item, red[1], tid, m);
-    if (nxt >= n_tiles) break;
-    tile = nxt;
-  }
-}
 
 // Generic path for shapes the item kernel does not take (n_cols % 64 != 0
 // for Q4_0/Q8_0): one wavefront per row, one 32-weight block per lane step,
@@ -597,127 +112,6 @@ __global__ void __launch_bounds__(256) gemv_generic_q6k_kernel(const uint8_t *__
   }
 }
 
-// Rows the item kernel takes: whole items, at most 2048 per row, and for
-// Q6_K an even number of blocks (4-byte aligned rows) and at most 1024
-// items (n_cols <= 65536).
-bool item_path_ok(uint32_t dt, int n_cols) {
-  if (n_cols / 64 > 2048) return false;
-  if (dt == SWAMP_Q4_K) return true;
-  if (dt == SWAMP_Q6_K) return n_cols % 512 == 0 && n_cols / 64 <= 1024;
-  return n_cols % 64 == 0;
-}
-
-// Launch shape: waves per CU the persistent grid aims for, and rows per
-// tile (SWAMP_GEMV_WAVES_PER_CU / SWAMP_GEMV_ROWS override them).
-struct Tuning {
-  int waves_per_cu = 4;
-  int rows = 0;  // 0: chosen per shape
-  Tuning() {
-    if (const char *s = std::getenv("SWAMP_GEMV_WAVES_PER_CU")) {
-      int v = std::atoi(s);
-      if (v >= 1 && v <= 64) waves_per_cu = v;
-    }
-    if (const char *s = std::getenv("SWAMP_GEMV_ROWS")) {
-      int v = std::atoi(s);
-      if (v == 1 || v == 2 || v == 4) rows = v;
-    }
-  }
-};
-const Tuning &tuning() {
-  static Tuning t;
-  return t;
-}
-
-template <int DT, int kPPT, int kRows, int kWaves>
-int launch_items(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
-  const int ipr = n_cols / 64;
-  if (ipr > kPPT * 64 * kWaves) return SWAMP_ESHAPE;
-  const int n_tiles = ms.tile_end[ms.n - 1];
-  const int cus = swamp::device_info().num_cus;
-  int grid = cus * std::max(1, tuning().waves_per_cu / kWaves);
-  if (grid > n_tiles) grid = n_tiles;
-  if (grid < 1) return SWAMP_OK;
-  if (ms.n == 1)
-    gemv_kernel<DT, kPPT, kRows, kWaves, false>
-        <<<grid, 64 * kWaves, 0, s>>>(ms, x, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
-  else
-    gemv_kernel<DT, kPPT, kRows, kWaves, true>
-        <<<grid, 64 * kWaves, 0, s>>>(ms, x, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
-  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
-}
-
-int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, const int *rows,
-                 int tile_rows) {
-  ms.n = n;
-  int acc = 0;
-  for (int i = 0; i < n; i++) {
-    ms.w[i] = static_cast<const uint8_t *>(ws[i]);
-    ms.y[i] = ys[i];
-    ms.rows[i] = rows[i];
-    acc += (rows[i] + tile_rows - 1) / tile_rows;
-    ms.tile_end[i] = acc;
-  }
-  return acc;
-}
-
-// Waves per workgroup for a row of ipr items (matches launch_rows).
-int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
-
-// Rows per tile: 4 when every workgroup of the grid gets at least 8 tiles,
-// else 2 when it gets at least 2, else 1; always 1 when a lane holds
-// several items (rows of more than 512 items).  Longer tile runs per wave
-// hide the first tile's latency and the x prologue; shorter tiles keep
-// small matrices spread over the whole chip.
-int tile_rows_for(int n_cols, int total_rows) {
-  const int ipr = n_cols / 64;
-  const int cap = ipr <= 512 ? 4 : 1;
-  if (tuning().rows) return std::min(tuning().rows, cap);
-  const int cus = swamp::device_info().num_cus;
-  const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(ipr));
-  int r = 1;
-  if (long(total_rows) / 4 >= 8 * slots) r = 4;
-  else if (long(total_rows) / 2 >= 2 * slots) r = 2;
-  return std::min(r, cap);
-}
-
-template <int DT, int kRows>
-int launch_rows(const MatSet &ms, const float *x, int n_cols, hipStream_t s) {
-  const int ipr = n_cols / 64;
-  if (ipr <= 64) return launch_items<DT, 1, kRows, 1>(ms, x, n_cols, s);
-  if (ipr <= 128) return launch_items<DT, 1, kRows, 2>(ms, x, n_cols, s);
-  if (ipr <= 256) return launch_items<DT, 1, kRows, 4>(ms, x, n_cols, s);
-  if (ipr <= 512) return launch_items<DT, 1, kRows, 8>(ms, x, n_cols, s);
-  // With several items per lane the tiles are single rows (tile_rows_for
-  // caps them) so both register buffers fit without spills; a Q6_K item
-  // (19 dwords per row buffer) allows at most two items per lane, longer
-  // Q6_K rows take the generic kernel (item_path_ok).
-  if constexpr (kRows > 1) return SWAMP_ESHAPE;
-  else if (ipr <= 1024) return launch_items<DT, 2, 1, 8>(ms, x, n_cols, s);
-  else if constexpr (DT == SWAMP_Q6_K) return SWAMP_ESHAPE;
-  else if (ipr <= 2048) return launch_items<DT, 4, 1, 8>(ms, x, n_cols, s);
-  return SWAMP_ESHAPE;
-}
-
-template <int DT>
-int launch_dt(const MatSet &ms, const float *x, int n_cols, int tile_rows, hipStream_t s) {
-  switch (tile_rows) {
-  case 4: return launch_rows<DT, 4>(ms, x, n_cols, s);
-  case 2: return launch_rows<DT, 2>(ms, x, n_cols, s);
-  default: return launch_rows<DT, 1>(ms, x, n_cols, s);
-  }
-}
-
-int dispatch(uint32_t dt, const MatSet &ms, const float *x, int n_cols, int tile_rows,
-             hipStream_t s) {
-  switch (dt) {
-  case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0>(ms, x, n_cols, tile_rows, s);
-  case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0>(ms, x, n_cols, tile_rows, s);
-  case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K>(ms, x, n_cols, tile_rows, s);
-  case SWAMP_Q6_K: return launch_dt<SWAMP_Q6_K>(ms, x, n_cols, tile_rows, s);
-  default: return SWAMP_EDTYPE;
-  }
-}
-
 }  // namespace
 
 int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
@@ -741,50 +135,13 @@ int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *
   MatSet ms;
   const void *ws[1] = {d_w};
   float *ys[1] = {d_y};
-  const int tr = tile_rows_for(n_cols, n_rows);
+  const int tr = tile_rows_for(dtype, n_cols, n_rows);
   build_matset(ms, 1, ws, ys, &n_rows, tr);
-  return dispatch(dtype, ms, d_x, n_cols, tr, s);
+  return dispatch<kProNone>(dtype, ms, d_x, Pro{}, n_cols, tr, s);
 }
 
 int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
                             const int *row_counts, const float *d_x, float *const *d_ys,
                             int n_cols, hipStream_t s) {
-  // Matrices of one dtype share a launch (and the x prologue); a different
-  // dtype starts another launch on the same stream.
-  bool done[kMaxMats] = {};
-  for (int i = 0; i < n_mats; i++) {
-    if (done[i]) continue;
-    const uint32_t dt = dtypes[i];
-    if (!item_path_ok(dt, n_cols)) {
-      for (int j = i; j < n_mats; j++)
-        if (!done[j] && dtypes[j] == dt) {
-          int rc = swamp_launch_gemv(dt, d_ws[j], d_x, d_ys[j], row_counts[j], n_cols, s);
-          if (rc) return rc;
-          done[j] = true;
-        }
-      continue;
-    }
-    const void *ws[kMaxMats];
-    float *ys[kMaxMats];
-    int rows[kMaxMats];
-    int n = 0, total = 0;
-    for (int j = i; j < n_mats; j++)
-      if (!done[j] && dtypes[j] == dt && row_counts[j] > 0) {
-        ws[n] = d_ws[j];
-        ys[n] = d_ys[j];
-        rows[n] = row_counts[j];
-        total += row_counts[j];
-        n++;
-        done[j] = true;
-      } else if (dtypes[j] == dt) {
-        done[j] = true;
-      }
-    if (n == 0) continue;
-    MatSet ms;
-    const int tr = tile_rows_for(n_cols, total);
-    build_matset(ms, n, ws, ys, rows, tr);
-    int rc = dispatch(dt, ms, d_x, n_cols, tr, s);
-    if (rc) return rc;
-  }
-  return SWAMP_OK;
+  return launch_multi<kProNone>(n_mats, dtypes, d_ws, row_counts, d_x, Pro{}, d_ys, n_cols, s);
 }

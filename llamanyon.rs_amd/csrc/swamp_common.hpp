@@ -92,7 +92,8 @@ const DeviceInfo &device_info();  // current device (initialises it)
 
 }  // namespace swamp
 
-// Internal launchers (defined in dequant.hip, gemv.hip, gemm.hip).  They
+// Internal launchers (defined in dequant.hip, gemv.hip, gemv_fused.hip,
+// gemv_batched.hip, gemm.hip, gemm_i8.hip).  They
 // assume the arguments have been validated by api.cpp.
 int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
                          size_t n, hipStream_t s);
@@ -102,6 +103,14 @@ int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes,
                             const void *const *d_ws, const int *row_counts,
                             const float *d_x, float *const *d_ys, int n_cols,
                             hipStream_t s);
+int swamp_launch_gemv_rmsnorm(int n_mats, const uint32_t *dtypes,
+                              const void *const *d_ws, const int *row_counts,
+                              const float *d_x, const float *d_norm_w, float eps,
+                              float *const *d_ys, int n_cols, hipStream_t s);
+int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w,
+                             const float *d_gate, const float *d_up, float *d_y,
+                             int n_rows, int n_cols, int accumulate,
+                             hipStream_t s);
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,
                               const float *d_x, float *d_y, int n_tok,
                               int n_rows, int n_cols, int accumulate,

@@ -52,6 +52,10 @@ def lib() -> ctypes.CDLL:
                                     c_size, i32]),
         "or_forward_linear_batch": (i32, [u32, c_vp, c_size, c_vp, c_vp, c_size, c_size, c_size,
                                           i32]),
+        "or_rmsnorm": (None, [c_vp, c_vp, c_vp, c_size, f32]),
+        "or_silu": (None, [c_vp, c_size]),
+        "or_mul_in_place": (None, [c_vp, c_vp, c_size]),
+        "or_add_in_place": (None, [c_vp, c_vp, c_size]),
         "or_gemv_q8_dot": (f32, [c_vp, c_vp, i32, f32]),
         "or_xorshift64_i8": (None, [ctypes.POINTER(ctypes.c_uint64), c_vp, c_size]),
     }
@@ -173,6 +177,35 @@ def forward_linear_batch(dtype: int, raw: np.ndarray, xs: np.ndarray, n_rows: in
     if rc != 0:
         raise ValueError(f"or_forward_linear_batch rc={rc}")
     return outs
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    assert x.size == w.size
+    out = np.empty_like(x)
+    lib().or_rmsnorm(_p(out), _p(x), _p(w), x.size, eps)
+    return out
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    out = np.array(x, dtype=np.float32, copy=True, order="C")
+    lib().or_silu(_p(out), out.size)
+    return out
+
+
+def mul_in_place(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = np.array(a, dtype=np.float32, copy=True, order="C")
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    lib().or_mul_in_place(_p(out), _p(b), out.size)
+    return out
+
+
+def add_in_place(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = np.array(a, dtype=np.float32, copy=True, order="C")
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    lib().or_add_in_place(_p(out), _p(b), out.size)
+    return out
 
 
 def gemv_q8_dot(w: np.ndarray, a: np.ndarray, scale: float) -> float:

@@ -7,6 +7,7 @@
  */
 #include "swamp_oracle.h"
 
+#include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -588,6 +589,41 @@ int or_forward_linear_batch(uint32_t dtype, const uint8_t *raw, size_t raw_len,
     if (rc != 0) return rc;
   }
   return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* f32 steps either side of the path, swamp-engine/src/ops.rs:188-220      */
+/* ---------------------------------------------------------------------- */
+
+/* rmsnorm, ops.rs:188-201: ss = sum x*x in order, ss /= n, ss += eps,
+ * inv = 1 / sqrt(ss), out = x * inv * w (left to right). */
+void or_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps) {
+  float ss = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    float p = x[i] * x[i];
+    ss = ss + p;
+  }
+  ss = ss / (float)n;
+  ss = ss + eps;
+  float inv = 1.0f / sqrtf(ss);
+  for (size_t i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* silu, ops.rs:203-208: x = x / (1 + exp(-x)), with the C library's expf
+ * (what f32::exp calls on Linux). */
+void or_silu(float *x, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    float v = x[i];
+    x[i] = v / (1.0f + expf(-v));
+  }
+}
+
+/* mul_in_place, ops.rs:210-214; add_in_place, ops.rs:216-220 */
+void or_mul_in_place(float *a, const float *b, size_t n) {
+  for (size_t i = 0; i < n; i++) a[i] = a[i] * b[i];
+}
+void or_add_in_place(float *a, const float *b, size_t n) {
+  for (size_t i = 0; i < n; i++) a[i] = a[i] + b[i];
 }
 
 /* ---------------------------------------------------------------------- */

@@ -109,6 +109,15 @@ int or_forward_linear_batch(uint32_t dtype, const uint8_t *raw, size_t raw_len,
                             const float *xs, float *outs, size_t bs,
                             size_t n_rows, size_t n_cols, int n_threads);
 
+/* The f32 steps the engine runs either side of the path
+ * (swamp-engine/src/ops.rs): rmsnorm (:188-201, sequential sum of squares,
+ * out = x * inv * w), silu in place (:203-208, libm expf), mul_in_place
+ * (:210-214), add_in_place (:216-220). */
+void or_rmsnorm(float *out, const float *x, const float *w, size_t n, float eps);
+void or_silu(float *x, size_t n);
+void or_mul_in_place(float *a, const float *b, size_t n);
+void or_add_in_place(float *a, const float *b, size_t n);
+
 /* swamp_gemv_q8_vnni scalar arm, swamp-kernels/src/lib.rs:452-482:
  * exact int32 dot of two int8 vectors times scale; null or k<=0 -> 0. */
 float or_gemv_q8_dot(const int8_t *w, const int8_t *a, int k, float scale);

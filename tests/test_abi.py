@@ -94,6 +94,24 @@ def test_argument_validation_precedes_device(pkg):
     assert L.swamp_qgemv_batched(pkg.Q6_K, fake, 1 << 20, fake, fake, 2, 4, 512, 1, None) == pkg.EDTYPE
     assert L.swamp_qgemm(pkg.Q6_K, fake, 1 << 20, fake, pkg.BF16, fake, 4, 4, 512, None) == pkg.EDTYPE
     assert L.swamp_qdequant(pkg.Q6_K, fake, 419, fake, 512, None) == pkg.ESHAPE
+    # fused prologues: one item per lane (n_cols <= 32768, whole items)
+    import ctypes
+    one = lambda T, v: (T * 1)(v)
+    def rms(dt, cols, norm=fake, x=fake, eps=1e-5):
+        return L.swamp_qgemv_rmsnorm(1, one(ctypes.c_uint32, dt), one(ctypes.c_void_p, fake),
+                                     one(ctypes.c_size_t, 1 << 30), one(ctypes.c_int, 4), x,
+                                     norm, eps, one(ctypes.c_void_p, fake), cols, None)
+    assert rms(pkg.Q4_0, 32832) == pkg.ESHAPE
+    assert rms(pkg.Q4_0, 96) == pkg.ESHAPE and rms(pkg.Q4_0, 0) == pkg.ESHAPE
+    assert rms(pkg.Q6_K, 256) == pkg.ESHAPE and rms(pkg.Q4_K, 320) == pkg.ESHAPE
+    assert rms(pkg.Q4_0, 4096, norm=None) == pkg.EINVAL
+    assert rms(pkg.Q4_0, 4096, norm=fake + 4) == pkg.EINVAL
+    assert rms(13, 4096) == pkg.EDTYPE
+    sw = lambda dt, cols, up=fake: L.swamp_qgemv_swiglu(dt, fake, 1 << 30, fake, up, fake, 4,
+                                                        cols, 1, None)
+    assert sw(pkg.Q8_0, 96) == pkg.ESHAPE and sw(pkg.Q8_0, 32832) == pkg.ESHAPE
+    assert sw(pkg.Q6_K, 768) == pkg.ESHAPE and sw(pkg.Q4_K, 0) == pkg.ESHAPE
+    assert sw(pkg.Q8_0, 4096, up=None) == pkg.EINVAL and sw(pkg.Q8_0, 4096, up=fake + 8) == pkg.EINVAL
     assert L.swamp_qdequant(pkg.Q4_0, fake, 35, fake, 64, None) == pkg.ESHAPE
     assert L.swamp_quantize_q8_0(fake, pkg.F32, fake, 33, None) == pkg.ESHAPE
     n = 9

@@ -105,7 +105,7 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
  * eps), each y_m OVERWRITTEN; x_norm is not written.  Replaces the
  * engine's rmsnorm (swamp-engine/src/ops.rs:188-201) followed by
  * forward_linear_multi / forward_linear on its output (executor.rs:433-445
- * QKV, :488-499 gate+up, :523-526 logits).  Arguments as swamp_qgemv_multi
+ * QKV, :488-499 gate+up, :530-533 logits).  Arguments as swamp_qgemv_multi
  * plus d_norm_w (n_cols floats, 16-byte aligned) and eps.  The sum of
  * squares is reduced in a different order than the reference's sequential
  * loop.  n_cols <= 32768 and a whole number of 64-weight items (multiple of
@@ -120,7 +120,7 @@ int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes,
  * projection): h = gate / (1 + exp(-gate)) * up, then y = W h
  * (accumulate = 0) or y += W h (accumulate = 1, the residual add).
  * Replaces silu + mul_in_place (swamp-engine/src/ops.rs:203-214) +
- * forward_linear + add_in_place (:216-220) at executor.rs:501-505.
+ * forward_linear + add_in_place (:216-220) at executor.rs:501-506.
  * d_gate, d_up: n_cols floats each, 16-byte aligned.  Shape rules as
  * swamp_qgemv_rmsnorm. */
 int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,

@@ -3,13 +3,13 @@
 //
 //  * RMSNorm -> GEMV: rmsnorm(x_norm, x, w_norm, eps) followed by
 //    forward_linear_multi / forward_linear on x_norm (swamp-engine/src/
-//    executor.rs:433-445 for QKV, :488-499 for gate+up, :523-526 for the
+//    executor.rs:433-445 for QKV, :488-499 for gate+up, :530-533 for the
 //    logits).  Every workgroup loads all of x anyway, so it computes the sum
 //    of squares itself (a 16 KB re-read from L2 per workgroup) and never
 //    writes x_norm.
 //  * SiLU * up -> down GEMV: silu(gate); mul_in_place(gate, up);
 //    forward_linear(down, gate) and, when accumulate is set, the residual
-//    add_in_place(x, ffn_down) (executor.rs:501-505): y += W h.
+//    add_in_place(x, ffn_down) (executor.rs:501-506): y += W h.
 //
 // Both keep one 64-weight item per lane (n_cols <= 32768), which covers the
 // hidden and intermediate sizes of the Llama family.

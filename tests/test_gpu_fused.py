@@ -1,7 +1,7 @@
 """GPU parity of the fused-prologue GEMVs against the oracle's composition of
 the engine's steps: rmsnorm (swamp-engine/src/ops.rs:188-201) then
 forward_linear per matrix (linear.rs:14-90, 96-170), and silu + mul_in_place
-+ forward_linear + add_in_place (ops.rs:203-220, executor.rs:501-505).
++ forward_linear + add_in_place (ops.rs:203-220, executor.rs:501-506).
 Gate: max_r |y - y_ref| / (||W_r|| ||x_fed||) <= 1e-3 with x_fed the oracle's
 normalized / gated vector.  Also the n_cols == 0 contract (y = 0)."""
 import numpy as np

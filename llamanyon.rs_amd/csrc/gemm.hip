@@ -7,29 +7,39 @@
 // computes y[m][r] = sum_k W[r,k] x[m][k] for the whole prompt.
 //
 // bf16 path (MFMA-bound: 2*M*N*K flops over ~0.56 B/weight + 2 B/act):
-//  * Workgroup tile 256 tokens x 256 weight rows, K step 64, 4 waves in a
-//    2 x 2 arrangement; each wave owns 128 x 128 outputs = 4 x 4
-//    V_MFMA_F32_32X32X16_BF16 tiles (256 fp32 accumulators per lane).
-//  * LDS: three activation stages and two dequantized-weight stages, 32 KB
-//    each (160 KB).  Activations go global -> LDS directly (buffer_load ...
-//    lds, no VGPRs, no LDS write instructions), two K steps ahead; weight
-//    items go to registers two steps ahead and are dequantized one step
-//    ahead into the other weight stage, in slices interleaved with the
-//    current step's MFMAs, so the vector ALU and LDS work hides under the
-//    matrix cores.  One barrier per step, which waits (in-order memory
-//    counter) for the next step's activations only.
-//  * Fragments of the next 16-wide k slice are read from LDS while the
-//    current slice's 16 MFMAs run.
-//  * Weight dequantization: lane t owns row t of the tile; one 64-weight
-//    item per step becomes 8 chunks of 8 bf16 (byte -> float converts, one
-//    fma each, packed RNE convert).
-//  * LDS rows are 128 B; 16-byte chunks are XOR-swizzled by row so the
-//    32-row fragment reads and the row-wise writes spread over the banks.
-//  * Workgroup ids are remapped so each XCD (ids i, i+8, ...) walks a
-//    contiguous run of tiles that share weight columns in its L2.
-//  * The tiles of an incomplete last round (all tiles, when there are fewer
-//    than CUs) are split along K across workgroups; those add into y
-//    (their blocks zeroed first) with hardware float atomics.
+//  * Workgroup tile 256 tokens x 256 weight rows (or a 128-token half tile,
+//    below), K step 64 (one 64-weight item per row), 8 waves = two per
+//    SIMD.  Wave w owns weight rows [32w, 32w + 32) and every token of the
+//    tile: 8 V_MFMA_F32_32X32X16_BF16 tiles, 128 fp32 accumulators.
+//  * Weights never touch LDS.  Each wave loads its own rows' items two K
+//    steps ahead and dequantizes them one step ahead straight into the
+//    B-operand layout (lane l: row 32w + l%32, k = 16s + 8(l/32) .. +7 of
+//    substep s), so every weight is converted once per tile.  With two
+//    waves per SIMD, one wave's dequantization issues while the other's
+//    MFMAs run (vector ALU work issued by the wave that also issues the
+//    MFMAs stretches the MFMA cadence; another wave's does not).
+//  * Activations: five LDS stages filled by direct-to-LDS DMA
+//    (buffer_load ... lds, no VGPRs) four K steps ahead; 128-byte rows
+//    with 16-byte chunks XOR-swizzled by (row / 2) % 8.  Each A fragment
+//    is re-read into its register right after the MFMA that consumed it.
+//    One barrier per K step; its wait covers the loads issued before the
+//    previous step (the memory counter is in order), so two steps of
+//    loads stay in flight.
+//  * Dequantization is q * s + o rounded once in fp32 by an fma (exact up
+//    to that rounding) and then to bf16: the same B values as the
+//    dequantization kernels produce, rounded to bf16.  Nibbles are masked
+//    in place (w & 0x0F0F0F0F, w & 0xF0F0F0F0) and read by the byte
+//    converts; the high nibbles come out as 16q and take s / 16 (exact).
+//  * Tile order: groups of 4 token tiles, consecutive tiles walking the
+//    weight columns of a group; workgroup ids are remapped so each XCD
+//    (ids i, i+8, ...) runs a contiguous run of that order.  A round of an
+//    XCD's 32 CUs then shares 4 activation slabs and 8 weight columns in
+//    its L2.
+//  * Decomposition: complete rounds of full tiles; a last round at most
+//    half full runs as twice as many 128-token half tiles (no partial
+//    sums); problems of at most half a round run as half tiles, and are
+//    split along K (pieces added into y with float atomics after zeroing)
+//    only when the half tiles still fill at most half the CUs.
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
 
@@ -47,22 +57,25 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
-constexpr int kThreads = 256;
-constexpr int kXStage = kBM * kBK * 2;              // 32 KB activations
-constexpr int kWStage = kBN * kBK * 2;              // 32 KB dequantized weights
-constexpr int kXOff = 0, kWOff = 3 * kXStage;        // 3 activation + 2 weight stages
-constexpr int kSmemBytes = 3 * kXStage + 2 * kWStage; // 160 KB
+constexpr int kBM = 256, kBN = 256, kBK = 64;  // full tile and K step
+constexpr int kThreads = 512, kWaves = 8;
+constexpr int kStages = 5;                     // activation stages
+constexpr int kGroup = 4;                      // token tiles per order group
 
-#ifndef SWAMP_GEMM_SWZ
-#define SWAMP_GEMM_SWZ 1
-#endif
+// Per-shape constants: kTok token tiles of 32 per wave (8: full tile,
+// 4: half tile).
+template <int DT, int kTok>
+struct Cfg {
+  static constexpr int kRows = 32 * kTok;              // tokens of the tile
+  static constexpr int kXStage = kRows * kBK * 2;      // bytes of one stage
+  static constexpr int kSmem = kStages * kXStage;      // 160 KB / 80 KB
+  static constexpr int kDma = kRows * 128 / 1024 / kWaves;  // 1 KB DMAs per wave and step
+  static constexpr int kWLoads = DT == SWAMP_Q8_0 ? 5 : 3;  // weight loads per item
+  static constexpr int kVmem = kDma + kWLoads;         // vector-memory ops per step
+};
+
 __device__ __forceinline__ int swz(int row, int chunk) {
-#if SWAMP_GEMM_SWZ == 1
   return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
-#else
-  return row * 128 + ((chunk ^ (row & 7)) << 4);
-#endif
 }
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -72,74 +85,107 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// byte j of w as a float (V_CVT_F32_UBYTEj)
-__device__ __forceinline__ float ubyte(uint32_t w, int j) { return float((w >> (8 * j)) & 0xFFu); }
+// One 16-byte-per-lane DMA into LDS (lane L writes lds + 16 L).  Not a
+// template: the host compilation pass rejects the LDS address-space cast
+// inside a template instantiation.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff,
+                                      uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                           voff, soff, 0, 0);
+}
 
-// Chunk c (weights 8c .. 8c+7 of the item, natural k order) dequantized to
-// 8 bf16.  Every value is q*s - o rounded once in fp32 (the fma is exact
-// up to that rounding), then rounded to bf16.
-template <int DT>
-__device__ __forceinline__ u32x4v_t dequant_chunk(const Raw<DT> &r, int item, int c) {
-  float v[8];
-  if constexpr (DT == SWAMP_Q4_0) {
-    // block c/4; chunk dword t = bytes 4t..4t+3 of the block's nibbles;
-    // element 2b = low nibble of byte b, 2b+1 = high nibble (q4_0.rs:30-35)
-    const int blk = c >> 2, t = c & 3;
-    const uint32_t w = blk == 0 ? shr16(r.d[t + 1], r.d[t]) : r.d[5 + t];
-    const float d = swamp::f16_bits_to_f32(blk == 0 ? (r.d[0] & 0xFFFFu) : (r.d[4] >> 16));
-    const float o = -8.0f * d;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+// Eight weights from the four bytes of w as 16q_hi / q_lo pairs: byte p
+// holds elements 2p (low nibble, scale s) and 2p + 1 (high nibble, read
+// as 16 q with scale s16 = s / 16); value q * s + o.  The empty asm keeps
+// the masked words opaque, so the byte converts read them directly
+// instead of re-extracting each nibble.
+__device__ __forceinline__ u32x4v_t deq_pairs(uint32_t w, float s, float s16, float o) {
+  uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+  asm("" : "+v"(lo), "+v"(hi));
+  u32x4v_t out;
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-      v[2 * b] = __builtin_fmaf(ubyte(lo, b), d, o);
-      v[2 * b + 1] = __builtin_fmaf(ubyte(hi, b), d, o);
+  for (int p = 0; p < 4; p++) {
+    const float a = float((lo >> (8 * p)) & 0xFFu), b = float((hi >> (8 * p)) & 0xFFu);
+    out[p] = pack_bf16(__builtin_fmaf(a, s, o), __builtin_fmaf(b, s16, o));
+  }
+  return out;
+}
+
+// Eight consecutive weights from the bytes of two words w0, w1 (byte i of
+// w0 is weight i), each byte u the weight's code; value u * s + o.
+__device__ __forceinline__ u32x4v_t deq_bytes(uint32_t w0, uint32_t w1, float s, float o) {
+  asm("" : "+v"(w0), "+v"(w1));
+  u32x4v_t out;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    out[p] = pack_bf16(__builtin_fmaf(float((w0 >> (16 * p)) & 0xFFu), s, o),
+                       __builtin_fmaf(float((w0 >> (16 * p + 8)) & 0xFFu), s, o));
+    out[2 + p] = pack_bf16(__builtin_fmaf(float((w1 >> (16 * p)) & 0xFFu), s, o),
+                           __builtin_fmaf(float((w1 >> (16 * p + 8)) & 0xFFu), s, o));
+  }
+  return out;
+}
+
+// B fragment of substep S for the lane's row: weights 16S + 8h .. +7 of
+// the item (h = lane / 32), i.e. 8-weight chunk c = 2S + h.  S is a
+// template argument so every index into the item is a constant: the item
+// array then lives in registers from the start, and a per-lane choice
+// between two of its words stays a register select.
+template <int DT, int S>
+__device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, int item, bool h) {
+  if constexpr (DT == SWAMP_Q4_0) {
+    // blocks at item bytes 0 and 18 (d, then 16 nibble bytes; byte b holds
+    // elements 2b and 2b + 1, q4_0.rs:30-35); chunk c's nibbles are bytes
+    // 4(c%4) .. +3 of its block: block 0's start 2 bytes into a dword
+    if constexpr (S < 2) {
+      constexpr int t = 2 * S;  // chunk 2S + h: dwords t + h and t + h + 1, shifted by 2 bytes
+      const uint32_t w = shr16(h ? r.d[t + 2] : r.d[t + 1], h ? r.d[t + 1] : r.d[t]);
+      const float d = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
+      return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
+    } else {
+      constexpr int t = 5 + 2 * (S - 2);
+      const uint32_t w = h ? r.d[t + 1] : r.d[t];
+      const float d = swamp::f16_bits_to_f32(r.d[4] >> 16);
+      return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
     }
   } else if constexpr (DT == SWAMP_Q8_0) {
-    const int blk = c >> 2, t = c & 3;
-    uint32_t w0, w1;
-    if (blk == 0) {
-      w0 = shr16(r.d[2 * t + 1], r.d[2 * t]);
-      w1 = shr16(r.d[2 * t + 2], r.d[2 * t + 1]);
+    // blocks at item bytes 0 and 34 (d, then 32 int8); chunk t = 2(S%2) + h
+    // of block S/2 is bytes 8t .. 8t+7 of its quants; bytes carry q + 128
+    // after the xor, value (q + 128) d - 128 d = q d exactly
+    if constexpr (S < 2) {
+      constexpr int t = 4 * S;  // chunk 2S starts at dword t (+2 bytes), 2S + 1 at t + 2
+      const uint32_t a = h ? r.d[t + 2] : r.d[t], b = h ? r.d[t + 3] : r.d[t + 1],
+                     c = h ? r.d[t + 4] : r.d[t + 2];
+      const float d = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
+      return deq_bytes(shr16(b, a) ^ 0x80808080u, shr16(c, b) ^ 0x80808080u, d, -128.0f * d);
     } else {
-      w0 = r.d[9 + 2 * t];
-      w1 = r.d[10 + 2 * t];
-    }
-    const float d = swamp::f16_bits_to_f32(blk == 0 ? (r.d[0] & 0xFFFFu) : (r.d[8] >> 16));
-    const float o = -128.0f * d;  // bytes carry q + 128
-    w0 ^= 0x80808080u;
-    w1 ^= 0x80808080u;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      v[b] = __builtin_fmaf(ubyte(w0, b), d, o);
-      v[4 + b] = __builtin_fmaf(ubyte(w1, b), d, o);
+      constexpr int t = 9 + 4 * (S - 2);
+      const uint32_t w0 = h ? r.d[t + 2] : r.d[t], w1 = h ? r.d[t + 3] : r.d[t + 1];
+      const float d = swamp::f16_bits_to_f32(r.d[8] >> 16);
+      return deq_bytes(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, -128.0f * d);
     }
   } else {
-    // chunk c < 4: sub-block A elements 8c.. = low nibbles of bytes 8c..;
-    // c >= 4: sub-block B = high nibbles of bytes 8(c-4).. (layout A,
-    // q4_k.rs:290-319)
-    const float d = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
+    // Q4_K quarter: sub-block A = low nibbles of the 32 bytes (S < 2),
+    // sub-block B = high nibbles (S >= 2) (layout A, q4_k.rs:290-319);
+    // chunk 2(S%2) + h covers bytes 8(2(S%2) + h) .. +7
+    const float dd = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
     q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
-    const bool hi = c >= 4;
-    const float s = d * float(hi ? sc1 : sc0), o = -(dmin * float(hi ? m1 : m0));
-    const int cc = c & 3;
-    const uint32_t w0 = hi ? (r.q[2 * cc] >> 4) : r.q[2 * cc];
-    const uint32_t w1 = hi ? (r.q[2 * cc + 1] >> 4) : r.q[2 * cc + 1];
-    const uint32_t a0 = w0 & 0x0F0F0F0Fu, a1 = w1 & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      v[b] = __builtin_fmaf(ubyte(a0, b), s, o);
-      v[4 + b] = __builtin_fmaf(ubyte(a1, b), s, o);
-    }
+    constexpr bool hb = S >= 2;
+    const float sc = dd * float(hb ? sc1 : sc0), o = -(dmin * float(hb ? m1 : m0));
+    constexpr int t = 4 * (S & 1);
+    const uint32_t w0 = h ? r.q[t + 2] : r.q[t], w1 = h ? r.q[t + 3] : r.q[t + 1];
+    // low nibbles: bytes of w & 0x0F0F0F0F; high: w & 0xF0F0F0F0 (16 q)
+    constexpr uint32_t mask = hb ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    return deq_bytes(w0 & mask, w1 & mask, hb ? 0.0625f * sc : sc, o);
   }
-  return u32x4v_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
-                  pack_bf16(v[6], v[7])};
 }
 
 // Raw bytes of one weight item through a buffer resource: the lane's row in
 // the VGPR offset, the item's byte offset within a row in the (uniform) SGPR
 // offset.  Reads past the descriptor's range return zeros.
+
 template <int DT>
 __device__ __forceinline__ void load_item(Raw<DT> &r, __amdgpu_buffer_rsrc_t rs, uint32_t vrow,
                                           int item) {
@@ -170,138 +216,138 @@ __device__ __forceinline__ void load_item(Raw<DT> &r, __amdgpu_buffer_rsrc_t rs,
   }
 }
 
-// Per-thread load geometry.  Activations go global -> LDS directly
-// (buffer_load ... lds): instruction i of wave w fills LDS bytes
-// [1024 (8w + i), +1024) of an activation stage = rows 8(8w+i) .. +7, lane L
-// writing row 8(8w+i) + L/8, physical 16-byte chunk L%8; the lane fetches
-// the logical chunk that the swizzle puts there.  The weight item is row
-// n0 + tid, through registers (it is dequantized).
+// Per-lane load geometry.  DMA instruction i of wave w fills stage bytes
+// [1024 (kDma w + i), +1024) = tile rows 8(kDma w + i) .. +7: lane L writes
+// row 8(kDma w + i) + L/8, physical chunk L%8, and fetches the logical chunk
+// the swizzle puts there, (L%8) ^ ((row / 2) % 8) = (L%8) ^ ((4i + L/16) % 8)
+// (kDma w is even).  The weight item of the lane is row 32w + L%32.
 struct Geo {
   __amdgpu_buffer_rsrc_t xr, wr;
-  uint32_t xv[2];   // per-lane VGPR offsets for even / odd instructions
-  uint32_t xs;      // m0 * K * 2 (scalar)
-  uint32_t xinst;   // 8 * K * 2: scalar step between instructions
-  uint32_t wv;      // per-lane weight row offset
+  uint32_t xv[2];  // per-lane DMA offsets for even / odd instructions
+  uint32_t xs;     // m0 * K * 2 (scalar)
+  uint32_t xinst;  // 8 * K * 2: scalar step between instructions
+  uint32_t wv;     // per-lane weight row offset
   int wave;
 };
 
-__device__ __forceinline__ void xdma(uint8_t *xstage, const Geo &g, int kt) {
+template <int kDma>
+__device__ __forceinline__ void xdma(uint8_t *stage, const Geo &g, int kt) {
 #pragma unroll
-  for (int i = 0; i < 8; i++)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        g.xr, (__attribute__((address_space(3))) void *)(xstage + 1024 * (8 * g.wave + i)), 16,
-        g.xv[i & 1], g.xs + uint32_t(i) * g.xinst + uint32_t(kt) * 128u, 0, 0);
+  for (int i = 0; i < kDma; i++)
+    dma16(g.xr, stage + 1024 * (kDma * g.wave + i), g.xv[i & 1],
+          g.xs + uint32_t(i) * g.xinst + uint32_t(kt) * 128u);
 }
 
-__device__ __forceinline__ void frags(const uint8_t *stg, const uint8_t *ws, int ks, int wm, int wn,
-                                      int lane, bf16x8_t (&a)[4], bf16x8_t (&b)[4]) {
-  const int fr = lane & 31, fc = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    a[i] = *reinterpret_cast<const bf16x8_t *>(stg + swz(wm * 128 + i * 32 + fr, 2 * ks + fc));
-#pragma unroll
-  for (int j = 0; j < 4; j++)
-    b[j] = *reinterpret_cast<const bf16x8_t *>(ws + swz(wn * 128 + j * 32 + fr, 2 * ks + fc));
+// A fragment of token tile i, substep ks (k = 16 ks + 8(l/32) .. +7).
+__device__ __forceinline__ bf16x8_t a_frag(const uint8_t *stg, int ks, int i, int lane) {
+  return *reinterpret_cast<const bf16x8_t *>(stg +
+                                             swz(32 * i + (lane & 31), 2 * ks + (lane >> 5)));
 }
 
-template <int DT>
-__host__ __device__ constexpr int wloads() {
-  return DT == SWAMP_Q8_0 ? 5 : 3;  // buffer loads per weight item
-}
-
-// One K step: MFMAs on activation stage xc and weight stage wc.  Meanwhile
-// step kt+2's activations stream into stage xf by DMA and its weight item
-// into registers `fetch`; step kt+1's weight item (registers `nw`, loaded a
-// step ago) is dequantized into weight stage wn.  The closing barrier waits
-// (in-order memory counter) for step kt+1's DMA only: the loads issued
-// after it -- kt+1's weights, kt+2's DMA and weights -- stay in flight.
-template <int DT>
-__device__ __forceinline__ void kstep(f32x16_t (&acc)[4][4], const uint8_t *xc, const uint8_t *wc,
-                                      uint8_t *xf, uint8_t *wn, const Raw<DT> &nw,
-                                      Raw<DT> &fetch, const Geo &g, int kt, int kt1, int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave & 1, wn_ = wave >> 1;
-  const int k1 = min(kt + 1, kt1 - 1), k2 = min(kt + 2, kt1 - 1);  // past the end: re-read
-  xdma(xf, g, k2);
-  __builtin_amdgcn_sched_barrier(0);
-  load_item<DT>(fetch, g.wr, g.wv, k2);
-  __builtin_amdgcn_sched_barrier(0);
-  bf16x8_t a[2][4], b[2][4];
-  frags(xc, wc, 0, wm, wn_, lane, a[0], b[0]);
-#pragma unroll
-  for (int ks = 0; ks < 4; ks++) {
-    const int p = ks & 1;
-    if (ks < 3) frags(xc, wc, ks + 1, wm, wn_, lane, a[p ^ 1], b[p ^ 1]);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p][i], b[p][j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-      const int c = 2 * ks + q;
-      *reinterpret_cast<u32x4v_t *>(wn + swz(tid, c)) = dequant_chunk<DT>(nw, k1, c);
-    }
-#pragma unroll
-    for (int m = 0; m < 16; m++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // 5 VALU
-      if (m < 8 && ks < 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-      if (m == 9 || m == 13) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // 1 DS write
-    }
-    __builtin_amdgcn_sched_barrier(0);
+// Substep KS of a K step (k = 16 KS .. 16 KS + 15): the MFMAs of every
+// token tile with B fragment bc[KS]; each A fragment is re-read right after
+// the MFMA that consumed it (for substep KS + 1, or the next step's
+// substep 0 from `nxt`); step kt+1's B fragment KS is dequantized from
+// `nw`.  Substep 0 also issues the step's loads: step kt+4's activations
+// into `dma`, step kt+2's weight item into `fetch`.
+template <int DT, int kTok, int KS>
+__device__ __forceinline__ void substep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
+                                        const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
+                                        const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
+                                        const Raw<DT> &nw, Raw<DT> &fetch, const Geo &g, int kt,
+                                        int kt1, int lane) {
+  using C = Cfg<DT, kTok>;
+  if constexpr (KS == 0) {
+    xdma<C::kDma>(dma, g, min(kt + kStages - 1, kt1 - 1));  // past the end: re-read
+    load_item<DT>(fetch, g.wr, g.wv, min(kt + 2, kt1 - 1));
   }
-  // wait for step kt+1's DMA (8 + 2 weight loads were issued after it)
-  constexpr int kAfter = 8 + 2 * wloads<DT>();
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kAfter) : "memory");
+#pragma unroll
+  for (int i = 0; i < kTok; i++) {
+    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], __builtin_bit_cast(bf16x8_t, bc[KS]),
+                                                     acc[i], 0, 0, 0);
+    a[i] = KS < 3 ? a_frag(cur, KS + 1, i, lane) : a_frag(nxt, 0, i, lane);
+  }
+  bn[KS] = b_frag<DT, KS>(nw, min(kt + 1, kt1 - 1), lane >= 32);
+#pragma unroll
+  for (int m = 0; m < kTok; m++) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 1 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // 1 DS read
+    __builtin_amdgcn_sched_group_barrier(0x002, 32 / kTok, 0);  // VALU
+    if constexpr (KS == 0)
+      __builtin_amdgcn_sched_group_barrier(0x010, (C::kVmem + kTok - 1) / kTok, 0);  // VMEM
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(
-    const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, float *__restrict__ y, int M,
-    int N, int K, size_t row_bytes, int tiles_m, int n_full, int splits, int kt_per_split) {
+// One K step.  a[] holds substep 0's A fragments on entry (read before the
+// previous barrier) and the next step's on return.
+template <int DT, int kTok>
+__device__ __forceinline__ void kstep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
+                                      const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
+                                      const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
+                                      const Raw<DT> &nw, Raw<DT> &fetch, const Geo &g, int kt,
+                                      int kt1, int lane) {
+  using C = Cfg<DT, kTok>;
+  substep<DT, kTok, 0>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 1>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 2>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 3>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  // The loads issued before the previous step -- among them step kt+2's
+  // activations -- are complete; the last kTok fragment reads (of `nxt`)
+  // stay in flight across the barrier.
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(%1)\n\ts_barrier" ::"n"(2 * C::kVmem),
+               "n"(kTok)
+               : "memory");
+}
+
+// Tile t of the grouped order -> (token tile, weight tile).
+__host__ __device__ inline void tile_coords(int t, int tiles_m, int tiles_n, int &mt, int &nt) {
+  const int grp = t / (kGroup * tiles_n), first = grp * kGroup;
+  const int gs = min(tiles_m - first, kGroup), r = t % (kGroup * tiles_n);
+  mt = first + r % gs;
+  nt = r / gs;
+}
+
+// Work of one launch: tiles [first, first + count) of the grouped order,
+// each as `parts` token parts (1: full tile, 2: halves) x `splits` K pieces.
+struct Work {
+  int tiles_m, tiles_n, first, parts, splits, kt_per_split;
+};
+
+template <int DT, int kTok>
+__global__ void __launch_bounds__(kThreads, 1)
+    gemm_bf16_kernel(const uint8_t *w, const uint16_t *x, float *__restrict__ y, int M, int N,
+                     int K, size_t row_bytes, Work wk) {
+  // w and x carry no __restrict__: the hand-counted waits assume every load
+  // is issued where the code places it, and with the weights known to be
+  // read-only the compiler may move their loads across the barriers (whose
+  // memory clobber then no longer orders them).
+  using C = Cfg<DT, kTok>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave & 1, wn = wave >> 1;
 
-  // Work items: tiles [0, n_full) with their whole K range, then `splits`
-  // K pieces of each remaining tile (added into y atomically; their y
-  // blocks are zeroed first).  XCD-aware order: hardware ids i, i+8, ...
-  // run on one XCD; each XCD gets a contiguous run of the (m-fastest) full
-  // tiles -- M tiles sharing a weight column share that XCD's L2 -- and an
-  // equal share of the pieces, which come last on every XCD.
-  const int n_work = int(gridDim.x);
-  const int n_piece = n_work - n_full;
-  int L = blockIdx.x;
-  if (n_full % 8 == 0 && n_piece % 8 == 0) {
-    const int xcd = L % 8, loc = L / 8, f8 = n_full / 8, p8 = n_piece / 8;
-    L = loc < f8 ? xcd * f8 + loc : n_full + xcd * p8 + (loc - f8);
-  }
+  // XCD-aware unit order: hardware ids i, i+8, ... run on one XCD; each
+  // XCD takes a contiguous run of units.
+  const int n_units = int(gridDim.x);
+  int u = blockIdx.x;
+  if (n_units % 8 == 0) u = (u % 8) * (n_units / 8) + u / 8;
+  const int per_tile = wk.parts * wk.splits;
+  const int t = wk.first + u / per_tile, part = (u % per_tile) / wk.splits;
+  const int piece = u % wk.splits;
+  int mt, nt;
+  tile_coords(t, wk.tiles_m, wk.tiles_n, mt, nt);
+  const int m0 = mt * kBM + part * C::kRows, n0 = nt * kBN;
+  if (m0 >= M) return;  // second half of a short last token tile (uniform)
   const int KT = K / kBK;
-  int tile, kt0, kt1, atomic;
-  if (L < n_full) {
-    tile = L;
-    kt0 = 0;
-    kt1 = KT;
-    atomic = 0;
-  } else {
-    const int q = L - n_full;
-    tile = n_full + q / splits;
-    kt0 = (q % splits) * kt_per_split;
-    kt1 = min(KT, kt0 + kt_per_split);
-    atomic = 1;
-  }
-  const int mt = tile % tiles_m, nt = tile / tiles_m;
-  const int m0 = mt * kBM, n0 = nt * kBN;
+  const int kt0 = piece * wk.kt_per_split, kt1 = min(KT, kt0 + wk.kt_per_split);
+  const bool atomic = wk.splits > 1;
 
   Geo g;
   g.wave = __builtin_amdgcn_readfirstlane(wave);
   g.xr = swamp::make_rsrc(x, uint32_t(size_t(M) * K * 2));
   {
-    // lane L of instruction i: row 8(8w+i) + L/8, physical chunk L%8,
-    // logical chunk (L%8) ^ ((row >> 1) & 7) = (L%8) ^ ((4i + L/16) & 7)
-    const int rl = wave * 64 + (lane >> 3);
+    const int rl = 8 * C::kDma * wave + (lane >> 3);
 #pragma unroll
     for (int par = 0; par < 2; par++) {
       const int c = (lane & 7) ^ ((4 * par + (lane >> 4)) & 7);
@@ -312,76 +358,79 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(
   g.xinst = uint32_t(8 * K * 2);
   const int nrows = min(kBN, N - n0);
   g.wr = swamp::make_rsrc(w + size_t(n0) * row_bytes, uint32_t(size_t(nrows) * row_bytes));
-  g.wv = uint32_t(size_t(tid) * row_bytes);
+  g.wv = uint32_t(size_t(32 * wave + (lane & 31)) * row_bytes);
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[kTok];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < kTok; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
 
-  uint8_t *const X0 = smem + kXOff, *const W0 = smem + kWOff;
-  auto xst = [&](int s) { return X0 + kXStage * s; };
-  auto wst = [&](int s) { return W0 + kWStage * s; };
-  Raw<DT> r0, r1;
-  // prologue: step kt0 -> X0 (DMA) and W0 (dequant); kt0+1 -> X1 (DMA) and r1
-  xdma(xst(0), g, kt0);
+  auto st = [&](int s) { return smem + C::kXStage * ((s - kt0) % kStages); };
+  Raw<DT> ra, rb;
+  u32x4v_t ba[4], bb[4];
+  bf16x8_t a[kTok];
+  const bool h = lane >= 32;
+  // Prologue in the steady-state order: x(kt0), x(kt0+1), x(kt0+2), w(kt0),
+  // x(kt0+3), w(kt0+1) (steps kt0-4 .. kt0-1 of the loop's pattern).
+  xdma<C::kDma>(st(kt0), g, kt0);
   __builtin_amdgcn_sched_barrier(0);
-  load_item<DT>(r0, g.wr, g.wv, kt0);
+  xdma<C::kDma>(st(kt0 + 1), g, min(kt0 + 1, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
-  xdma(xst(1), g, min(kt0 + 1, kt1 - 1));
+  xdma<C::kDma>(st(kt0 + 2), g, min(kt0 + 2, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
-  load_item<DT>(r1, g.wr, g.wv, min(kt0 + 1, kt1 - 1));
+  load_item<DT>(ra, g.wr, g.wv, kt0);
   __builtin_amdgcn_sched_barrier(0);
+  xdma<C::kDma>(st(kt0 + 3), g, min(kt0 + 3, kt1 - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  load_item<DT>(rb, g.wr, g.wv, min(kt0 + 1, kt1 - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  ba[0] = b_frag<DT, 0>(ra, kt0, h);
+  ba[1] = b_frag<DT, 1>(ra, kt0, h);
+  ba[2] = b_frag<DT, 2>(ra, kt0, h);
+  ba[3] = b_frag<DT, 3>(ra, kt0, h);
+  // x(kt0) and x(kt0+1) complete: 2 kVmem loads were issued after x(kt0+1)
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * C::kVmem) : "memory");
 #pragma unroll
-  for (int c = 0; c < 8; c++)
-    *reinterpret_cast<u32x4v_t *>(wst(0) + swz(tid, c)) = dequant_chunk<DT>(r0, kt0, c);
-  {
-    // step kt0's DMA done: kt0's weights, kt0+1's DMA and weights follow it
-    constexpr int kAfter = 8 + 2 * wloads<DT>();
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(kAfter) : "memory");
-  }
+  for (int i = 0; i < kTok; i++) a[i] = a_frag(st(kt0), 0, i, lane);
 
-  // Two steps per trip (static register roles); LDS stages rotate with the
-  // step: activations kt%3, weights kt%2 (counted from kt0).
+  // Two steps per trip so the register buffers keep static roles.
+  constexpr int D = kStages - 1;
   int kt = kt0;
   for (; kt + 1 < kt1; kt += 2) {
-    const int j = kt - kt0;
-    kstep<DT>(acc, xst(j % 3), wst(0), xst((j + 2) % 3), wst(1), r1, r0, g, kt, kt1, tid);
-    kstep<DT>(acc, xst((j + 1) % 3), wst(1), xst((j + 3) % 3), wst(0), r0, r1, g, kt + 1, kt1, tid);
+    kstep<DT, kTok>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
+    kstep<DT, kTok>(acc, a, st(kt + 1), st(kt + 2), st(kt + 1 + D), bb, ba, ra, rb, g, kt + 1,
+                    kt1, lane);
   }
-  if (kt < kt1) {
-    const int j = kt - kt0;
-    kstep<DT>(acc, xst(j % 3), wst(0), xst((j + 2) % 3), wst(1), r1, r0, g, kt, kt1, tid);
-  }
+  if (kt < kt1)
+    kstep<DT, kTok>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
 
   // C layout of a 32x32 tile: lane holds column (lane & 31), rows
   // 8*(e/4) + 4*(lane/32) + (e%4) for e = 0..15.
   const int fr = lane & 31, fc = lane >> 5;
+  const int n = n0 + 32 * wave + fr;
+  if (n < N) {
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n = n0 + wn * 128 + j * 32 + fr;
+    for (int i = 0; i < kTok; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int m = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * fc + (e & 3);
-        if (m < M && n < N) {
+        const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * fc + (e & 3);
+        if (m < M) {
           float *dst = y + size_t(m) * N + n;
-          if (atomic) unsafeAtomicAdd(dst, acc[i][j][e]);
-          else *dst = acc[i][j][e];
+          if (atomic) unsafeAtomicAdd(dst, acc[i][e]);
+          else *dst = acc[i][e];
         }
       }
-    }
+  }
 }
 
-// Zero the y blocks of tiles [first, first + gridDim.x / 64): block b
-// clears 4 rows of tile first + b/64, each thread 4 consecutive floats.
-__global__ void zero_tiles_kernel(float *__restrict__ y, int M, int N, int tiles_m, int first) {
-  const int tile = first + int(blockIdx.x) / 64;
-  const int mt = tile % tiles_m, nt = tile / tiles_m;
+// Zero the y blocks of tiles [first, first + gridDim.x / 64) of the grouped
+// order: block b clears 4 rows of tile first + b/64, each thread 4 floats.
+__global__ void zero_tiles_kernel(float *__restrict__ y, int M, int N, int tiles_m, int tiles_n,
+                                  int first) {
+  const int t = first + int(blockIdx.x) / 64;
+  int mt, nt;
+  tile_coords(t, tiles_m, tiles_n, mt, nt);
   const int m = mt * kBM + 4 * (int(blockIdx.x) % 64) + int(threadIdx.x) / 64;
   const int n = nt * kBN + 4 * (int(threadIdx.x) % 64);
   if (m >= M) return;
@@ -423,15 +472,55 @@ __global__ void quantize_q8_0_kernel(const void *__restrict__ src, uint8_t *__re
   }
 }
 
-template <int DT>
-int set_smem_attr() {
+template <int DT, int kTok>
+int launch_tiles(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows, int n_cols,
+                 const Work &wk, int count, hipStream_t s) {
+  using C = Cfg<DT, kTok>;
   static std::once_flag once;
   static hipError_t err = hipSuccess;
   std::call_once(once, [] {
-    err = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_bf16_kernel<DT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
+    err = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_bf16_kernel<DT, kTok>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmem);
   });
-  return err == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+  if (err != hipSuccess) return SWAMP_ELAUNCH;
+  const unsigned units = unsigned(count * wk.parts * wk.splits);
+  gemm_bf16_kernel<DT, kTok><<<units, kThreads, C::kSmem, s>>>(
+      w, x, y, m, n_rows, n_cols, swamp::row_bytes(DT, size_t(n_cols)), wk);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
+
+template <int DT>
+int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows, int n_cols,
+                hipStream_t s) {
+  const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
+  const int tiles = tiles_m * tiles_n, KT = n_cols / kBK;
+  const int cus = swamp::device_info().num_cus;
+  // Full tiles in complete rounds; the rest as 128-token halves when they
+  // fill at most one round; K pieces when even the halves leave more than
+  // half the CUs idle (pieces at least 8 steps long).
+  int n_full = tiles, n_half = 0, splits = 1;
+  if (tiles >= cus) {
+    const int rem = tiles % cus;
+    if (rem > 0 && 2 * rem <= cus) n_half = rem;
+  } else if (2 * tiles <= cus) {
+    n_half = tiles;
+    if (4 * tiles <= cus) splits = std::max(1, std::min({cus / (2 * tiles), 4, KT / 8}));
+  }
+  n_full = tiles - n_half;
+  const int kt_per_split = (KT + splits - 1) / splits;
+  splits = (KT + kt_per_split - 1) / kt_per_split;
+  if (n_full > 0) {
+    const Work wk{tiles_m, tiles_n, 0, 1, 1, KT};
+    if (int rc = launch_tiles<DT, 8>(w, x, y, m, n_rows, n_cols, wk, n_full, s)) return rc;
+  }
+  if (n_half > 0) {
+    if (splits > 1)
+      zero_tiles_kernel<<<unsigned(n_half * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n,
+                                                              n_full);
+    const Work wk{tiles_m, tiles_n, n_full, 2, splits, kt_per_split};
+    if (int rc = launch_tiles<DT, 4>(w, x, y, m, n_rows, n_cols, wk, n_half, s)) return rc;
+  }
+  return SWAMP_OK;
 }
 
 }  // namespace
@@ -442,53 +531,16 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   if (x_type == SWAMP_Q8_0) return swamp_launch_gemm_i8(dtype, d_w, d_x, d_y, m, n_rows, n_cols, s);
   if (x_type != SWAMP_BF16) return SWAMP_EDTYPE;
   if (n_cols % kBK != 0) return SWAMP_ESHAPE;
-  const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
-  const int tiles = tiles_m * tiles_n;
-  const int KT = n_cols / kBK;
-  // Balance the last round over the CUs (one workgroup per CU).  Split
-  // pieces of a tile add into y with float atomics, which cost about as
-  // much as a quarter of a round when every tile of a full round is split
-  // (measured), so: fewer tiles than half the CUs -> every tile splits
-  // along K into min(cus / tiles, 4) pieces; a last round at most half
-  // full -> its tiles split in 2; otherwise no split.  Pieces are at least
-  // 8 K steps long.
-  const int cus = swamp::device_info().num_cus;
-  const int rem = tiles % cus;
-  int n_full = tiles, splits = 1;
-  if (tiles * 2 <= cus) {
-    splits = std::min({cus / tiles, 4, KT / 8});
-    n_full = 0;
-  } else if (tiles > cus && rem > 0 && rem * 2 <= cus) {
-    splits = std::min(2, KT / 8);
-    n_full = tiles - rem;
-  }
-  splits = std::max(1, splits);
-  const int kt_per_split = (KT + splits - 1) / splits;
-  splits = (KT + kt_per_split - 1) / kt_per_split;
-  if (splits <= 1) n_full = tiles;
-  const int n_work = n_full + (tiles - n_full) * splits;
-  if (n_full < tiles)
-    zero_tiles_kernel<<<unsigned((tiles - n_full) * 64), 256, 0, s>>>(d_y, m, n_rows, tiles_m, n_full);
-  const dim3 grid{unsigned(n_work), 1u, 1u};
+  // activation offsets are 32-bit (buffer descriptors)
+  if (size_t(m) * size_t(n_cols) * 2 > size_t(UINT32_MAX)) return SWAMP_ESHAPE;
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint16_t *x = static_cast<const uint16_t *>(d_x);
-  const size_t rb = swamp::row_bytes(int(dtype), size_t(n_cols));
   switch (dtype) {
-#define SWAMP_GEMM_CASE(DT)                                                                    \
-  case DT:                                                                                     \
-    if (int rc = set_smem_attr<DT>()) return rc;                                               \
-    gemm_bf16_kernel<DT><<<grid, kThreads, kSmemBytes, s>>>(w, x, d_y, m, n_rows, n_cols, rb,  \
-                                                            tiles_m, n_full, splits,           \
-                                                            kt_per_split);                     \
-    break;
-    SWAMP_GEMM_CASE(SWAMP_Q4_0)
-    SWAMP_GEMM_CASE(SWAMP_Q8_0)
-    SWAMP_GEMM_CASE(SWAMP_Q4_K)
-#undef SWAMP_GEMM_CASE
-  default:
-    return SWAMP_EDTYPE;
+    case SWAMP_Q4_0: return launch_bf16<SWAMP_Q4_0>(w, x, d_y, m, n_rows, n_cols, s);
+    case SWAMP_Q8_0: return launch_bf16<SWAMP_Q8_0>(w, x, d_y, m, n_rows, n_cols, s);
+    case SWAMP_Q4_K: return launch_bf16<SWAMP_Q4_K>(w, x, d_y, m, n_rows, n_cols, s);
+    default: return SWAMP_EDTYPE;
   }
-  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
 
 int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n,

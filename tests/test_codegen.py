@@ -62,6 +62,86 @@ def _staged_wait(body):
     return None
 
 
+_VMEM = re.compile(r"\b(buffer_load|global_load|flat_load)")
+
+
+def _gemm_kernels(lines):
+    cur, body = None, []
+    for line in lines:
+        m = re.match(r"^(_ZN12_GLOBAL__N_116gemm_bf16_kernel\w+):", line)
+        if m:
+            cur, body = m.group(1), []
+            continue
+        if cur is not None:
+            body.append(line)
+            if "s_endpgm" in line:
+                yield cur, body
+                cur = None
+
+
+def _gemm_wait_problems(body):
+    """Checks the prefill GEMM's hand-counted waits.  The prologue issues
+    four activation DMA groups and two weight items in the order x0 x1 x2
+    w0 x3 w1 and then waits with vmcnt(N): N must be the number of loads
+    after x1, i.e. 2 P with P = loads per K step.  Each K step of the main
+    loop (two per trip) issues P loads and closes with vmcnt(2 P) +
+    s_barrier, which leaves exactly the previous and the current step's
+    loads in flight.  (The odd last step after the loop may issue fewer:
+    its weight prefetch is dead and removed.)"""
+    bars = [i for i, l in enumerate(body) if l.strip().startswith("s_barrier")]
+
+    def wait_before(b):
+        for j in range(b - 1, max(b - 4, -1), -1):
+            m = re.search(r"vmcnt\((\d+)\)", body[j])
+            if m:
+                return int(m.group(1))
+        return None
+
+    probs = []
+    pro = [l for l in body[:bars[0]] if _VMEM.search(l)]
+    dmas = [l for l in pro if l.rstrip().endswith(" lds")]
+    k_dma = len(dmas) // 4
+    p = (len(pro) - 2 * k_dma) // 2
+    if len(dmas) != 4 * k_dma or not all(l.rstrip().endswith(" lds") for l in pro[:2 * k_dma]):
+        probs.append("prologue does not start with two DMA groups")
+    if wait_before(bars[0]) != 2 * p:
+        probs.append("prologue wait %s != %d" % (wait_before(bars[0]), 2 * p))
+    head = [i for i, l in enumerate(body) if "Loop Header" in l]
+    if not head:
+        return probs + ["no K loop found"]
+    label = body[head[0]].split(":")[0]
+    back = [i for i, l in enumerate(body)
+            if re.match(r"\s+s_(c)?branch", l) and re.search(re.escape(label) + r"\b", l)]
+    if not back:
+        return probs + ["no K loop back-branch"]
+    lo, hi = head[0], back[-1]
+    loop_bars = [b for b in bars if lo < b < hi]
+    if len(loop_bars) != 2:
+        probs.append("%d barriers in the K loop, expected 2" % len(loop_bars))
+    prev = lo
+    for b in loop_bars:
+        loads = sum(1 for l in body[prev:b] if _VMEM.search(l))
+        n = wait_before(b)
+        if loads != p or n != 2 * p:
+            probs.append("step with %d loads waits vmcnt(%s), expected %d / %d" % (loads, n, p, 2 * p))
+        prev = b
+    # no full drain inside the K loop, no scratch traffic anywhere
+    if any("vmcnt(0)" in l for l in body[lo:hi + 1]):
+        probs.append("vmcnt(0) inside the K loop")
+    if any("scratch_" in l for l in body):
+        probs.append("scratch memory access")
+    return probs
+
+
+def test_gemm_wait_counts_match_emitted_loads(tmp_path):
+    lines = _asm("gemm.hip", str(tmp_path / "gemm.s"))
+    kernels = list(_gemm_kernels(lines))
+    # three weight formats x (full tile, half tile)
+    assert len(kernels) == 6, [k for k, _ in kernels]
+    bad = [(name, p) for name, body in kernels for p in [_gemm_wait_problems(body)] if p]
+    assert not bad, bad
+
+
 def test_staged_x_wait_counts_match_emitted_loads(tmp_path):
     tus = ["gemv.hip", "gemv_fused.hip"]
     with ThreadPoolExecutor(2) as ex:

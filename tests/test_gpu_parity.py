@@ -335,6 +335,40 @@ def test_gemm_bf16_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
     assert orc.normalized_error(y[toks], ref, deq, x_fed[toks]) <= TOL
 
 
+# Every work decomposition of the bf16 GEMM (256-token x 256-row tiles on
+# the CUs of one MI355X): complete rounds of full tiles; full tiles plus a
+# last round of 128-token half tiles (ragged tokens and rows: the second
+# half of the short last token tile is empty); one partial round of full
+# tiles; half tiles only, without a K split.
+DECOMP_CASES = [(2048, 8192, 4096), (1900, 28572, 4096), (2048, 6144, 4096), (2048, 4096, 14336)]
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("m,rows,cols", DECOMP_CASES)
+def test_gemm_bf16_decompositions(pkg, orc, torch_dev, dtype, m, rows, cols):
+    torch = torch_dev
+    raw = weights(pkg, dtype, rows, cols, mid=rows ^ m)
+    x = acts(pkg, m, cols, mid=m ^ cols)
+    xb = pkg.to_bf16_bits(x)
+    x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
+    say("gemm bf16 decomposition", dtype, m, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, xb.view(np.int16))
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), BF16, d_y.data_ptr(), m, rows,
+              cols, stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.all(np.isfinite(y))
+    # tokens at tile and half-tile edges, rows at both ends and the middle
+    toks = sorted(set([0, 127, 128, 255, 256, m // 2, m - 129, m - 128, m - 1]))
+    rb = pkg.row_bytes(dtype, cols)
+    for r0, r1 in [(0, 384), (rows // 2 - 128, rows // 2 + 128), (rows - 300, rows)]:
+        sub = raw[r0 * rb:r1 * rb]
+        ref = orc.forward_linear_batch(dtype, sub, x_fed[toks], r1 - r0, cols, 8)
+        deq = orc.dequantize(dtype, sub, (r1 - r0) * cols).reshape(r1 - r0, cols)
+        assert orc.normalized_error(y[toks, r0:r1], ref, deq, x_fed[toks]) <= TOL, (r0, r1)
+
+
 def test_gemm_rows_tail_and_token_consistency(pkg, orc, torch_dev):
     """GEMM token rows equal the per-token GEMV within tolerance; a ragged
     row count (not a tile multiple) leaves no NaN."""

@@ -30,6 +30,7 @@
 //    order (deterministic) after a barrier; nothing crosses workgroups.
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
@@ -237,13 +238,21 @@ struct Args {
   int lwk;         // log2 of Wk, the waves that share one tile (K slices)
   int phases;      // K phases; phase p covers items [p*ipp, p*ipp + ipp), ipp = ipw * Wk
   int accumulate;  // y += W x instead of y = W x
+  int nkg;         // K groups: workgroups split the row's items into nkg ranges
+  int ipk;         // items per K group (one phase each when nkg > 1)
+  float *ws;       // nkg > 1: partial sums [nkg][n_tok][n_rows], reduced afterwards
 };
 
-// y[t][row0 + r] += / = v for the tokens and rows that exist.
-__device__ __forceinline__ void put_y(const Args &a, int t, int row, float v) {
+// y[t][row0 + r] += / = v for the tokens and rows that exist; with K groups
+// the K group's partial sum goes to the workspace instead.
+__device__ __forceinline__ void put_y(const Args &a, int kg, int t, int row, float v) {
   if (t < a.n_tok && row < a.n_rows) {
-    float *d = a.y + size_t(t) * a.n_rows + row;
-    *d = a.accumulate ? *d + v : v;
+    if (a.nkg > 1) {
+      a.ws[(size_t(kg) * a.n_tok + t) * a.n_rows + row] = v;
+    } else {
+      float *d = a.y + size_t(t) * a.n_rows + row;
+      *d = a.accumulate ? *d + v : v;
+    }
   }
 }
 
@@ -315,7 +324,10 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   const int ipp = a.ipw << a.lwk;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
   const int n_tg = (n_tiles + wt - 1) / wt;
-  const int G = gridDim.x, b = blockIdx.x;
+  // with K groups the grid is nkg blocks of G workgroups; workgroup b of
+  // K group kg covers items [kg * ipk, kg * ipk + ipk) of its tiles
+  const int G = gridDim.x / a.nkg, b = blockIdx.x % G, kg = blockIdx.x / G;
+  const int kitem0 = kg * a.ipk;
   const int J = (n_tg - 1 - b) / G + 1;  // tile groups of this workgroup (b < n_tg)
   const int cpw = a.ipw / (4 * kChunk);  // chunks per wave, tile and phase
   const int n_chunks = a.phases * cpw * J;
@@ -346,7 +358,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
     const int tile = min(tile_of(q.batch, q.j), n_tiles - 1);
     const int row0 = tile * kRowsTile;
     // this wave's items in the chunk: base + g + 4*(c*kChunk + i)
-    const int base = q.p * ipp + ks * a.ipw;
+    const int base = kitem0 + q.p * ipp + ks * a.ipw;
     const int first = base + 4 * q.c * kChunk;  // first item of the chunk
     const uint32_t soff = uint32_t(base / 4) * quad_bytes<DT>() + uint32_t(q.c) * chunk_bytes;
     if constexpr (!kRagged) {
@@ -375,7 +387,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   issue(ra, qi);
   advance(qi);
   __builtin_amdgcn_sched_barrier(0);
-  stage_x<DT, TOK, 4>(a, xl, 0, ipp, tid);
+  stage_x<DT, TOK, 4>(a, xl, kitem0, ipp, tid);
   __syncthreads();
 
   const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * TOK + (r16 % TOK);
@@ -392,7 +404,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
     if (wk == 1) {
       if (tile < n_tiles) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) put_y(a, 4 * g + i, tile * kRowsTile + r16, v[i]);
+        for (int i = 0; i < 4; i++) put_y(a, kg, 4 * g + i, tile * kRowsTile + r16, v[i]);
       }
       return;
     }
@@ -406,7 +418,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       float sum = 0.f;
       for (int s2 = 0; s2 < wk; s2++) sum += src[s2 * 256];
       const int otile = (b + (batch * kJmax + k) * G) * wt + otl;
-      if (otile < n_tiles) put_y(a, e >> 4, otile * kRowsTile + (e & 15), sum);
+      if (otile < n_tiles) put_y(a, kg, e >> 4, otile * kRowsTile + (e & 15), sum);
     }
     lds_barrier();
   };
@@ -420,7 +432,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   auto consume = [&](const Raw<DT> (&r)[kChunk]) {
     if (P > 1 && qc.c == 0 && qc.j == 0 && (qc.p | qc.batch) != 0) {
       lds_barrier();  // every wave is done with the previous phase
-      stage_x<DT, TOK, 1>(a, xl, qc.p * ipp, ipp, tid);
+      stage_x<DT, TOK, 1>(a, xl, kitem0 + qc.p * ipp, ipp, tid);
       lds_barrier();
     }
     const half8_t *xc = xlane + qc.c * kChunk * 32 * TOK;
@@ -463,10 +475,22 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   }
 }
 
+// Sum of the K groups' partials, in K-group order (deterministic):
+// y = sum, or y += sum with accumulate.
+__global__ void kgroup_reduce_kernel(const float *__restrict__ ws, float *__restrict__ y, int nkg,
+                                     size_t n, int accumulate) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = ws[i];
+  for (int k = 1; k < nkg; k++) s += ws[size_t(k) * n + i];
+  y[i] = accumulate ? y[i] + s : s;
+}
+
 // Launch geometry: tokens in LDS, items per register chunk, waves per tile,
-// K phases.
+// K phases (nkg == 1) or K groups (nkg > 1: every workgroup owns one tile
+// group and one K range, staged once; the partials go to a.ws).
 template <int DT, int TOK, int kChunk, bool kRagged>
-int launch_geo(Args a, int lwk, hipStream_t s) {
+int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
   auto kern = gemv_batched_kernel<DT, TOK, kChunk, kRagged>;
   static std::once_flag once;
   std::call_once(once, [&] {
@@ -476,18 +500,73 @@ int launch_geo(Args a, int lwk, hipStream_t s) {
   const int q = 4 * kChunk;                           // item granule of a wave's K slice
   const int xcap = kXLdsMax / (TOK * 8 * 16);         // items of activations in LDS
   const int wk = 1 << lwk;
-  const int ipp_max = xcap / (q * wk) * (q * wk);
-  a.phases = (a.ipr + ipp_max - 1) / ipp_max;
-  const int per_phase = (a.ipr + a.phases - 1) / a.phases;
-  const int ipp = (per_phase + q * wk - 1) / (q * wk) * (q * wk);
+  const int gran = q * wk;
+  int ipp;
+  if (nkg > 1) {
+    a.ipk = ((a.ipr + nkg - 1) / nkg + gran - 1) / gran * gran;
+    if (a.ipk > xcap / gran * gran) return SWAMP_ESHAPE;  // chosen so that it fits
+    a.nkg = (a.ipr + a.ipk - 1) / a.ipk;
+    a.phases = 1;
+    ipp = a.ipk;
+  } else {
+    const int ipp_max = xcap / gran * gran;
+    a.nkg = 1;
+    a.ipk = 0;
+    a.phases = (a.ipr + ipp_max - 1) / ipp_max;
+    const int per_phase = (a.ipr + a.phases - 1) / a.phases;
+    ipp = (per_phase + gran - 1) / gran * gran;
+  }
   a.ipw = ipp / wk;
   a.lwk = lwk;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
   const int n_tg = (n_tiles + (kWaves >> lwk) - 1) / (kWaves >> lwk);
-  const int grid = std::min(n_tg, swamp::device_info().num_cus);
+  const int grid = (a.nkg > 1 ? n_tg : std::min(n_tg, swamp::device_info().num_cus)) * a.nkg;
   const size_t lds = size_t(ipp) * 8 * TOK * 16 + (wk > 1 ? kSlotBytes : 0);
   kern<<<unsigned(grid), kThreads, lds, s>>>(a);
-  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+  if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+  if (a.nkg > 1) {
+    const size_t n = size_t(a.n_tok) * a.n_rows;
+    kgroup_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(a.ws, a.y, a.nkg, n,
+                                                                   a.accumulate);
+    if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+  }
+  return SWAMP_OK;
+}
+
+// K-group plan of a pass: with one wave per tile (Wk = 1) a workgroup
+// covers 16 tiles; when those tile groups fill at most half the CUs and the
+// pass's activations are large (n_tok * K >= 32768 fp32, which the K-phase
+// form would stage whole into every workgroup), the row's items are split
+// over workgroups instead, each staging only its range: as many groups as
+// fill the CUs, each a multiple of the chunk granule q (8 items, or 4 when
+// that fills more CUs) and within the LDS.  nkg = 1: no split.
+struct KgPlan {
+  int nkg, q;
+};
+KgPlan kg_plan(int n_tok, int n_rows, int n_cols, int tok) {
+  static const int forced = [] {  // tuning override: SWAMP_BATCHED_NKG (1 = off)
+    const char *e = std::getenv("SWAMP_BATCHED_NKG");
+    return e ? std::atoi(e) : 0;
+  }();
+  const int ipr = (n_cols + 63) / 64;
+  const int cus = swamp::device_info().num_cus;
+  const int n_tg0 = ((n_rows + kRowsTile - 1) / kRowsTile + kWaves - 1) / kWaves;
+  const int xcap_items = kXLdsMax / (tok * 8 * 16);
+  if (forced == 1) return {1, 8};
+  if (forced <= 0 && (2 * n_tg0 > cus || long(n_tok) * n_cols < 32768)) return {1, 8};
+  KgPlan best{1, 8};
+  for (int q : {8, 4}) {
+    const int xcap = xcap_items / q * q;
+    if (q > xcap || q > ipr) continue;
+    int nkg = forced > 0 ? std::min(forced, ipr / q) : std::min(cus / n_tg0, ipr / q);
+    while (nkg >= 1 && nkg < ipr / q && (ipr + nkg - 1) / nkg > xcap) nkg++;
+    if (nkg < 2 || (forced <= 0 && n_tg0 * nkg > cus)) continue;
+    // the groups actually launched (ranges rounded up to the granule)
+    const int ipk = ((ipr + nkg - 1) / nkg + q - 1) / q * q;
+    const int used = (ipr + ipk - 1) / ipk;
+    if (used > best.nkg) best = {used, q};
+  }
+  return best;
 }
 
 // Waves per tile: the power of two that minimises the estimated time,
@@ -498,6 +577,17 @@ int launch_pass_tok(Args a, hipStream_t s) {
   const int cus = swamp::device_info().num_cus;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
   const int xcap = kXLdsMax / (TOK * 8 * 16);
+  if (a.ws) {
+    const KgPlan kp = kg_plan(a.n_tok, a.n_rows, a.n_cols, TOK);
+    const int nkg = kp.nkg, q = kp.q;
+    if (nkg > 1) {
+      if (q == 8)
+        return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, 0, nkg, s)
+                         : launch_geo<DT, TOK, 2, false>(a, 0, nkg, s);
+      return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, 0, nkg, s)
+                       : launch_geo<DT, TOK, 1, false>(a, 0, nkg, s);
+    }
+  }
   static const int forced = [] {  // tuning override: SWAMP_BATCHED_LWK (0..4)
     const char *e = std::getenv("SWAMP_BATCHED_LWK");
     return e ? std::atoi(e) : -1;
@@ -520,8 +610,52 @@ int launch_pass_tok(Args a, hipStream_t s) {
   // else fewer slices.
   while (best > 0 && ((4 << best) > xcap || (4 << best) > a.ipr)) best--;
   if ((8 << best) <= xcap && (8 << best) <= a.ipr)
-    return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, s) : launch_geo<DT, TOK, 2, false>(a, best, s);
-  return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, best, s) : launch_geo<DT, TOK, 1, false>(a, best, s);
+    return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, 1, s)
+                     : launch_geo<DT, TOK, 2, false>(a, best, 1, s);
+  return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, best, 1, s)
+                   : launch_geo<DT, TOK, 1, false>(a, best, 1, s);
+}
+
+// Token count of the pass's activation layout (4, 8 or 16).
+int pass_tok(int n_tok) { return n_tok <= 4 ? 4 : n_tok <= 8 ? 8 : 16; }
+
+// K groups a pass of n_tok tokens will use (the plan launch_pass_tok follows).
+int pass_kgroups(int n_tok, int n_rows, int n_cols) {
+  return kg_plan(n_tok, n_rows, n_cols, pass_tok(n_tok)).nkg;
+}
+
+// The K groups' partial sums live in a workspace kept per (device,
+// stream): calls on one stream run in order, so they can share it, and
+// calls on different streams never do.  It grows when a larger one is
+// needed (after the stream's queued work has finished with the old one)
+// and is kept for the life of the process.
+float *stream_workspace(hipStream_t s, size_t bytes) {
+  struct Entry {
+    int dev;
+    hipStream_t s;
+    float *p;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  for (Entry &e : cache) {
+    if (e.dev != dev || e.s != s) continue;
+    if (e.bytes >= bytes) return e.p;
+    if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
+    (void)hipFree(e.p);
+    e.p = nullptr;
+    e.bytes = 0;
+    if (hipMalloc(reinterpret_cast<void **>(&e.p), bytes) != hipSuccess) return e.p = nullptr;
+    e.bytes = bytes;
+    return e.p;
+  }
+  float *p = nullptr;
+  if (hipMalloc(reinterpret_cast<void **>(&p), bytes) != hipSuccess) return nullptr;
+  cache.push_back(Entry{dev, s, p, bytes});
+  return p;
 }
 
 template <int DT>
@@ -557,18 +691,26 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   a.accumulate = accumulate;
   // 16 rows of a tile are addressed by one buffer descriptor (32-bit range)
   if (size_t(a.row_bytes) * kRowsTile >= (size_t(1) << 30)) return SWAMP_ESHAPE;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return SWAMP_EDTYPE;
+  // workspace for the passes that split K over workgroups
+  size_t ws_bytes = 0;
   for (int t0 = 0; t0 < n_tok; t0 += kTok) {
+    const int nt = std::min(kTok, n_tok - t0);
+    const int nkg = pass_kgroups(nt, n_rows, n_cols);
+    if (nkg > 1) ws_bytes = std::max(ws_bytes, size_t(nkg) * nt * n_rows * sizeof(float));
+  }
+  // without a workspace the passes run as K phases
+  a.ws = ws_bytes ? stream_workspace(s, ws_bytes) : nullptr;
+  int rc = SWAMP_OK;
+  for (int t0 = 0; t0 < n_tok && rc == SWAMP_OK; t0 += kTok) {
     a.n_tok = std::min(kTok, n_tok - t0);
     a.x = d_x + size_t(t0) * n_cols;
     a.y = d_y + size_t(t0) * n_rows;
-    int rc;
     switch (dtype) {
     case SWAMP_Q4_0: rc = launch_pass<SWAMP_Q4_0>(a, s); break;
     case SWAMP_Q8_0: rc = launch_pass<SWAMP_Q8_0>(a, s); break;
-    case SWAMP_Q4_K: rc = launch_pass<SWAMP_Q4_K>(a, s); break;
-    default: return SWAMP_EDTYPE;
+    default: rc = launch_pass<SWAMP_Q4_K>(a, s); break;
     }
-    if (rc) return rc;
   }
-  return SWAMP_OK;
+  return rc;
 }

@@ -476,13 +476,20 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
 }
 
 // Sum of the K groups' partials, in K-group order (deterministic):
-// y = sum, or y += sum with accumulate.
+// y = sum, or y += sum with accumulate.  Up to 16 partials are loaded
+// before any is added, so their latencies overlap.
 __global__ void kgroup_reduce_kernel(const float *__restrict__ ws, float *__restrict__ y, int nkg,
                                      size_t n, int accumulate) {
   const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  float s = ws[i];
-  for (int k = 1; k < nkg; k++) s += ws[size_t(k) * n + i];
+  float s = 0.f;
+  for (int k0 = 0; k0 < nkg; k0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = k0 + j < nkg ? ws[size_t(k0 + j) * n + i] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += v[j];  // adding 0 past nkg leaves s unchanged
+  }
   y[i] = accumulate ? y[i] + s : s;
 }
 
@@ -535,14 +542,17 @@ int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
 
 // K-group plan of a pass: with one wave per tile (Wk = 1) a workgroup
 // covers 16 tiles; when those tile groups fill at most half the CUs and the
-// pass's activations are large (n_tok * K >= 32768 fp32, which the K-phase
-// form would stage whole into every workgroup), the row's items are split
-// over workgroups instead, each staging only its range: as many groups as
-// fill the CUs, each a multiple of the chunk granule q (8 items, or 4 when
-// that fills more CUs) and within the LDS.  nkg = 1: no split.
+// pass's activations are not small (n_tok * K >= 16384 fp32, which the
+// K-phase form would stage whole into every workgroup), the row's items are
+// split over workgroups instead, each staging only its range: as many
+// groups as fill the CUs (at least 4), each a multiple of the chunk granule
+// q (8 items, or 4 when that fills more CUs) and within the LDS.  nkg = 1:
+// no split.
 struct KgPlan {
   int nkg, q;
 };
+constexpr long kKgMinX = 16384;  // n_tok * K from which K groups pay (measured)
+constexpr int kKgMin = 4;        // fewer groups do not pay for the reduction (measured)
 KgPlan kg_plan(int n_tok, int n_rows, int n_cols, int tok) {
   static const int forced = [] {  // tuning override: SWAMP_BATCHED_NKG (1 = off)
     const char *e = std::getenv("SWAMP_BATCHED_NKG");
@@ -553,14 +563,14 @@ KgPlan kg_plan(int n_tok, int n_rows, int n_cols, int tok) {
   const int n_tg0 = ((n_rows + kRowsTile - 1) / kRowsTile + kWaves - 1) / kWaves;
   const int xcap_items = kXLdsMax / (tok * 8 * 16);
   if (forced == 1) return {1, 8};
-  if (forced <= 0 && (2 * n_tg0 > cus || long(n_tok) * n_cols < 32768)) return {1, 8};
+  if (forced <= 0 && (2 * n_tg0 > cus || long(n_tok) * n_cols < kKgMinX)) return {1, 8};
   KgPlan best{1, 8};
   for (int q : {8, 4}) {
     const int xcap = xcap_items / q * q;
     if (q > xcap || q > ipr) continue;
     int nkg = forced > 0 ? std::min(forced, ipr / q) : std::min(cus / n_tg0, ipr / q);
     while (nkg >= 1 && nkg < ipr / q && (ipr + nkg - 1) / nkg > xcap) nkg++;
-    if (nkg < 2 || (forced <= 0 && n_tg0 * nkg > cus)) continue;
+    if (nkg < 2 || (forced <= 0 && (n_tg0 * nkg > cus || nkg < kKgMin))) continue;
     // the groups actually launched (ranges rounded up to the granule)
     const int ipk = ((ipr + nkg - 1) / nkg + q - 1) / q * q;
     const int used = (ipr + ipk - 1) / ipk;

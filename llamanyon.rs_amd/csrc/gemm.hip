@@ -130,9 +130,11 @@ __device__ __forceinline__ u32x4v_t deq_bytes(uint32_t w0, uint32_t w1, float s,
 // the item (h = lane / 32), i.e. 8-weight chunk c = 2S + h.  S is a
 // template argument so every index into the item is a constant: the item
 // array then lives in registers from the start, and a per-lane choice
-// between two of its words stays a register select.
-template <int DT, int S>
-__device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, int item, bool h) {
+// between two of its words stays a register select.  Q = item % 4 (the
+// Q4_K quarter, whose sub-block scales the item uses) is one too, so the
+// scale unpacking has no branch.
+template <int DT, int S, int Q>
+__device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, bool h) {
   if constexpr (DT == SWAMP_Q4_0) {
     // blocks at item bytes 0 and 18 (d, then 16 nibble bytes; byte b holds
     // elements 2b and 2b + 1, q4_0.rs:30-35); chunk c's nibbles are bytes
@@ -171,7 +173,7 @@ __device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, int item, bool h) {
     const float dd = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
-    q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
+    q4k_scales(r.h, 2 * Q, sc0, m0, sc1, m1);  // Q: the item's quarter, a constant
     constexpr bool hb = S >= 2;
     const float sc = dd * float(hb ? sc1 : sc0), o = -(dmin * float(hb ? m1 : m0));
     constexpr int t = 4 * (S & 1);
@@ -250,7 +252,7 @@ __device__ __forceinline__ bf16x8_t a_frag(const uint8_t *stg, int ks, int i, in
 // substep 0 from `nxt`); step kt+1's B fragment KS is dequantized from
 // `nw`.  Substep 0 also issues the step's loads: step kt+4's activations
 // into `dma`, step kt+2's weight item into `fetch`.
-template <int DT, int kTok, int KS>
+template <int DT, int kTok, int KS, int Q>
 __device__ __forceinline__ void substep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
                                         const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
                                         const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
@@ -267,7 +269,7 @@ __device__ __forceinline__ void substep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTo
                                                      acc[i], 0, 0, 0);
     a[i] = KS < 3 ? a_frag(cur, KS + 1, i, lane) : a_frag(nxt, 0, i, lane);
   }
-  bn[KS] = b_frag<DT, KS>(nw, min(kt + 1, kt1 - 1), lane >= 32);
+  bn[KS] = b_frag<DT, KS, Q>(nw, lane >= 32);
 #pragma unroll
   for (int m = 0; m < kTok; m++) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 1 MFMA
@@ -280,18 +282,20 @@ __device__ __forceinline__ void substep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTo
 }
 
 // One K step.  a[] holds substep 0's A fragments on entry (read before the
-// previous barrier) and the next step's on return.
-template <int DT, int kTok>
+// previous barrier) and the next step's on return.  Q = (kt + 1) % 4, the
+// quarter of the item dequantized in this step (used by Q4_K; past the last
+// step the re-read item's B fragments are never used).
+template <int DT, int kTok, int Q>
 __device__ __forceinline__ void kstep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
                                       const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
                                       const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
                                       const Raw<DT> &nw, Raw<DT> &fetch, const Geo &g, int kt,
                                       int kt1, int lane) {
   using C = Cfg<DT, kTok>;
-  substep<DT, kTok, 0>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
-  substep<DT, kTok, 1>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
-  substep<DT, kTok, 2>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
-  substep<DT, kTok, 3>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 0, Q>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 1, Q>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 2, Q>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
+  substep<DT, kTok, 3, Q>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
   // The loads issued before the previous step -- among them step kt+2's
   // activations -- are complete; the last kTok fragment reads (of `nxt`)
   // stay in flight across the barrier.
@@ -385,25 +389,39 @@ __global__ void __launch_bounds__(kThreads, 1)
   __builtin_amdgcn_sched_barrier(0);
   load_item<DT>(rb, g.wr, g.wv, min(kt0 + 1, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
-  ba[0] = b_frag<DT, 0>(ra, kt0, h);
-  ba[1] = b_frag<DT, 1>(ra, kt0, h);
-  ba[2] = b_frag<DT, 2>(ra, kt0, h);
-  ba[3] = b_frag<DT, 3>(ra, kt0, h);
+  ba[0] = b_frag<DT, 0, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
+  ba[1] = b_frag<DT, 1, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
+  ba[2] = b_frag<DT, 2, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
+  ba[3] = b_frag<DT, 3, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
   // x(kt0) and x(kt0+1) complete: 2 kVmem loads were issued after x(kt0+1)
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * C::kVmem) : "memory");
 #pragma unroll
   for (int i = 0; i < kTok; i++) a[i] = a_frag(st(kt0), 0, i, lane);
 
-  // Two steps per trip so the register buffers keep static roles.
   constexpr int D = kStages - 1;
   int kt = kt0;
-  for (; kt + 1 < kt1; kt += 2) {
-    kstep<DT, kTok>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
-    kstep<DT, kTok>(acc, a, st(kt + 1), st(kt + 2), st(kt + 1 + D), bb, ba, ra, rb, g, kt + 1,
-                    kt1, lane);
+  if constexpr (DT == SWAMP_Q4_K) {
+    // Four steps per trip: the item quarters are constants (kt0 and kt1 are
+    // multiples of 4 for Q4_K, whose rows are whole 256-weight blocks).
+    for (; kt < kt1; kt += 4) {
+      kstep<DT, kTok, 1>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
+      kstep<DT, kTok, 2>(acc, a, st(kt + 1), st(kt + 2), st(kt + 1 + D), bb, ba, ra, rb, g,
+                         kt + 1, kt1, lane);
+      kstep<DT, kTok, 3>(acc, a, st(kt + 2), st(kt + 3), st(kt + 2 + D), ba, bb, rb, ra, g,
+                         kt + 2, kt1, lane);
+      kstep<DT, kTok, 0>(acc, a, st(kt + 3), st(kt + 4), st(kt + 3 + D), bb, ba, ra, rb, g,
+                         kt + 3, kt1, lane);
+    }
+  } else {
+    // Two steps per trip so the register buffers keep static roles.
+    for (; kt + 1 < kt1; kt += 2) {
+      kstep<DT, kTok, 0>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
+      kstep<DT, kTok, 0>(acc, a, st(kt + 1), st(kt + 2), st(kt + 1 + D), bb, ba, ra, rb, g,
+                         kt + 1, kt1, lane);
+    }
+    if (kt < kt1)
+      kstep<DT, kTok, 0>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
   }
-  if (kt < kt1)
-    kstep<DT, kTok>(acc, a, st(kt), st(kt + 1), st(kt + D), ba, bb, rb, ra, g, kt, kt1, lane);
 
   // C layout of a 32x32 tile: lane holds column (lane & 31), rows
   // 8*(e/4) + 4*(lane/32) + (e%4) for e = 0..15.
@@ -507,7 +525,8 @@ int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows
     if (4 * tiles <= cus) splits = std::max(1, std::min({cus / (2 * tiles), 4, KT / 8}));
   }
   n_full = tiles - n_half;
-  const int kt_per_split = (KT + splits - 1) / splits;
+  int kt_per_split = (KT + splits - 1) / splits;
+  if (DT == SWAMP_Q4_K) kt_per_split = (kt_per_split + 3) / 4 * 4;  // whole blocks per piece
   splits = (KT + kt_per_split - 1) / kt_per_split;
   if (n_full > 0) {
     const Work wk{tiles_m, tiles_n, 0, 1, 1, KT};

@@ -84,7 +84,7 @@ def _gemm_wait_problems(body):
     four activation DMA groups and two weight items in the order x0 x1 x2
     w0 x3 w1 and then waits with vmcnt(N): N must be the number of loads
     after x1, i.e. 2 P with P = loads per K step.  Each K step of the main
-    loop (two per trip) issues P loads and closes with vmcnt(2 P) +
+    loop (two per trip, four for Q4_K) issues P loads and closes with vmcnt(2 P) +
     s_barrier, which leaves exactly the previous and the current step's
     loads in flight.  (The odd last step after the loop may issue fewer:
     its weight prefetch is dead and removed.)"""
@@ -116,8 +116,8 @@ def _gemm_wait_problems(body):
         return probs + ["no K loop back-branch"]
     lo, hi = head[0], back[-1]
     loop_bars = [b for b in bars if lo < b < hi]
-    if len(loop_bars) != 2:
-        probs.append("%d barriers in the K loop, expected 2" % len(loop_bars))
+    if len(loop_bars) not in (2, 4):  # two steps per trip (four for Q4_K)
+        probs.append("%d barriers in the K loop, expected 2 or 4" % len(loop_bars))
     prev = lo
     for b in loop_bars:
         loads = sum(1 for l in body[prev:b] if _VMEM.search(l))

@@ -171,10 +171,14 @@ __device__ __forceinline__ half8_t weights_step(const Raw<DT> &r, int st, const 
     const half2_t d2 = as_h2(dbits | (dbits << 16));
     const half2_t off = {_Float16(-1152.0f), _Float16(-1152.0f)};
     const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128
-    o[0] = as_u((as_h2((u0 & 0x00FF00FFu) | kF16Magic) + off) * d2);
-    o[1] = as_u((as_h2(((u0 >> 8) & 0x00FF00FFu) | kF16Magic) + off) * d2);
-    o[2] = as_u((as_h2((u1 & 0x00FF00FFu) | kF16Magic) + off) * d2);
-    o[3] = as_u((as_h2(((u1 >> 8) & 0x00FF00FFu) | kF16Magic) + off) * d2);
+    // fp16 pairs (1024 + byte) built by one byte permute each: bytes 0 and
+    // 2 (or 1 and 3) of u under 0x64 high bytes from the magic word
+    constexpr uint32_t kSelEven = 0x07020500u, kSelOdd = 0x07030501u;
+    const uint32_t mg = 0x64646464u;
+    o[0] = as_u((as_h2(__builtin_amdgcn_perm(mg, u0, kSelEven)) + off) * d2);
+    o[1] = as_u((as_h2(__builtin_amdgcn_perm(mg, u0, kSelOdd)) + off) * d2);
+    o[2] = as_u((as_h2(__builtin_amdgcn_perm(mg, u1, kSelEven)) + off) * d2);
+    o[3] = as_u((as_h2(__builtin_amdgcn_perm(mg, u1, kSelOdd)) + off) * d2);
   } else {
     const half2_t off = {_Float16(-1024.0f), _Float16(-1024.0f)};
     const uint32_t w = r.q[st];

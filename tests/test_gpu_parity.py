@@ -291,6 +291,44 @@ def test_batched_repeat_bitwise(pkg, torch_dev):
                 assert np.array_equal(y.view(np.uint32), first[j].view(np.uint32)), (rep, j)
 
 
+def test_batched_two_streams(pkg, torch_dev):
+    """Matrices with few rows split K over workgroups through a workspace
+    kept per (device, stream): calls queued on two streams at once give the
+    same bits as the same calls run one after another on one stream."""
+    torch = torch_dev
+    cases = [(Q4_K, 16, 4096, 14336), (Q4_0, 8, 6144, 4096), (Q8_0, 12, 4096, 4096)]
+    bufs = []
+    for i, (dt, n_tok, rows, cols) in enumerate(cases):
+        raw = weights(pkg, dt, rows, cols, mid=120 + i)
+        xs = acts(pkg, n_tok, cols, mid=120 + i)
+        bufs.append((dt, n_tok, rows, cols, up(torch, raw), raw.size, up(torch, xs)))
+    say("batched two streams", len(cases))
+
+    def run(b, d_y, s):
+        dt, n_tok, rows, cols, d_w, wl, d_x = b
+        pkg.qgemv_batched(dt, d_w.data_ptr(), wl, d_x.data_ptr(), d_y.data_ptr(), n_tok, rows,
+                          cols, False, s)
+
+    ref = []
+    for b in bufs:
+        d_y = torch.full((b[1], b[2]), float("nan"), dtype=torch.float32, device="cuda")
+        run(b, d_y, stream(torch))
+        torch.cuda.synchronize()
+        ref.append(down(d_y))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
+    outs = [[torch.full((b[1], b[2]), float("nan"), dtype=torch.float32, device="cuda")
+             for b in bufs] for _ in range(2)]
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for j, b in enumerate(bufs):
+            run(b, outs[0][j], s1.cuda_stream)
+            run(bufs[-1 - j], outs[1][len(bufs) - 1 - j], s2.cuda_stream)
+    torch.cuda.synchronize()
+    for k in range(2):
+        for j in range(len(bufs)):
+            assert np.array_equal(down(outs[k][j]).view(np.uint32), ref[j].view(np.uint32)), (k, j)
+
+
 @pytest.mark.parametrize("cols", [4096, 14336])
 def test_batched_accumulate(pkg, orc, torch_dev, cols):
     """accumulate=1 is the kernel contract of fused_gemv_q4k_batched

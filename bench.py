@@ -18,7 +18,7 @@ Also reported (outside the timed steps):
     with HIP events recorded on the launch stream around each of its
     launches inside the timed region;
   * per-matrix GB/s (each matrix timed alone, outside the timed region);
-  * the Q4_0 prefill GEMM at 2048 tokens on the matrix cores, with bf16
+  * the Q4_0 prefill GEMM at 2048 and 512 tokens on the matrix cores, with bf16
     activations (fraction of the 2.5 PFLOP/s dense bf16 peak) and with
     Q8_0-quantized activations on the int8 MFMA (quantizer included;
     fraction of the 5.0 POP/s dense int8 peak);
@@ -57,7 +57,7 @@ DECODE_SHAPES = [              # (name, rows, K), Llama-3-8B, Q4_0
     ("lm_head", 128256, 4096),
 ]
 PREFILL_SHAPES = [("gate_up", 28672, 4096), ("down", 4096, 14336), ("qkv", 6144, 4096)]
-PREFILL_M = 2048
+PREFILL_MS = (2048, 512)        # prompt lengths of the prefill GEMM lines
 SEED = 0x5EED
 
 
@@ -409,56 +409,57 @@ def main():
                        "GB/s": round(b / (us * 1e-6) / 1e9, 1),
                        "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
 
-    # ---- prefill GEMM, 2048 tokens, bf16 activations ----------------------
+    # ---- prefill GEMM, 2048 and 512 tokens, bf16 / Q8_0 activations ----------
     prefill = None
     if not args.no_prefill:
         prefill = []
-        for i, (name, rows, k) in enumerate(PREFILL_SHAPES):
-            raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x100 ^ i, 0.02, rows, k)
-            w = torch.from_numpy(raw).cuda()
-            xf = pkg.fill_normal(SEED ^ 0x200 ^ i, 1.0, PREFILL_M, k)
-            xb = pkg.to_bf16_bits(xf)
-            x = torch.from_numpy(xb.view(np.int16)).cuda()
-            # int8 variant: the same activations quantized per 32-block to
-            # Q8_0 on the device (the quantizer is timed with the GEMM)
-            xf_d = torch.from_numpy(xf).cuda()
-            xq = torch.empty(PREFILL_M * k // 32 * 34, dtype=torch.uint8, device="cuda")
-            y = torch.empty((PREFILL_M, rows), dtype=torch.float32, device="cuda")
+        for pm in PREFILL_MS:
+            for i, (name, rows, k) in enumerate(PREFILL_SHAPES):
+                raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x100 ^ i, 0.02, rows, k)
+                w = torch.from_numpy(raw).cuda()
+                xf = pkg.fill_normal(SEED ^ 0x200 ^ i, 1.0, pm, k)
+                xb = pkg.to_bf16_bits(xf)
+                x = torch.from_numpy(xb.view(np.int16)).cuda()
+                # int8 variant: the same activations quantized per 32-block to
+                # Q8_0 on the device (the quantizer is timed with the GEMM)
+                xf_d = torch.from_numpy(xf).cuda()
+                xq = torch.empty(pm * k // 32 * 34, dtype=torch.uint8, device="cuda")
+                y = torch.empty((pm, rows), dtype=torch.float32, device="cuda")
 
-            def g_bf16():
-                rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), x.data_ptr(), pkg.BF16,
-                                     y.data_ptr(), PREFILL_M, rows, k, s)
-                if rc != 0:
-                    raise pkg.GpuError(rc, "swamp_qgemm")
+                def g_bf16():
+                    rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), x.data_ptr(),
+                                         pkg.BF16, y.data_ptr(), pm, rows, k, s)
+                    if rc != 0:
+                        raise pkg.GpuError(rc, "swamp_qgemm")
 
-            def g_int8():
-                rc = lib.swamp_quantize_q8_0(xf_d.data_ptr(), pkg.F32, xq.data_ptr(),
-                                             PREFILL_M * k, s)
-                if rc == 0:
-                    rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xq.data_ptr(),
-                                         pkg.Q8_0, y.data_ptr(), PREFILL_M, rows, k, s)
-                if rc != 0:
-                    raise pkg.GpuError(rc, "swamp_qgemm int8")
+                def g_int8():
+                    rc = lib.swamp_quantize_q8_0(xf_d.data_ptr(), pkg.F32, xq.data_ptr(),
+                                                 pm * k, s)
+                    if rc == 0:
+                        rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xq.data_ptr(),
+                                             pkg.Q8_0, y.data_ptr(), pm, rows, k, s)
+                    if rc != 0:
+                        raise pkg.GpuError(rc, "swamp_qgemm int8")
 
-            for xname, g, peak in (("bf16", g_bf16, BF16_PEAK_TFLOPS),
-                                   ("q8_0 (int8 MFMA)", g_int8, INT8_PEAK_TOPS)):
-                for _ in range(3):
-                    g()
-                reps = 10
-                e0, e1 = (torch.cuda.Event(enable_timing=True),
-                          torch.cuda.Event(enable_timing=True))
-                e0.record(stream)
-                for _ in range(reps):
-                    g()
-                e1.record(stream)
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / reps
-                tops = 2.0 * PREFILL_M * rows * k / (us * 1e-6) / 1e12
-                prefill.append({"name": name, "m": PREFILL_M, "rows": rows, "k": k, "x": xname,
-                                "us": round(us, 1), "TFLOP/s": round(tops, 1),
-                                "frac_peak": round(tops / peak, 4),
-                                "peak": peak})
-            del w, x, y, xf_d, xq
+                for xname, g, peak in (("bf16", g_bf16, BF16_PEAK_TFLOPS),
+                                       ("q8_0 (int8 MFMA)", g_int8, INT8_PEAK_TOPS)):
+                    for _ in range(3):
+                        g()
+                    reps = 10
+                    e0, e1 = (torch.cuda.Event(enable_timing=True),
+                              torch.cuda.Event(enable_timing=True))
+                    e0.record(stream)
+                    for _ in range(reps):
+                        g()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    us = e0.elapsed_time(e1) * 1e3 / reps
+                    tops = 2.0 * pm * rows * k / (us * 1e-6) / 1e12
+                    prefill.append({"name": name, "m": pm, "rows": rows, "k": k, "x": xname,
+                                    "us": round(us, 1), "TFLOP/s": round(tops, 1),
+                                    "frac_peak": round(tops / peak, 4),
+                                    "peak": peak})
+                del w, x, y, xf_d, xq
 
     cpu = None if args.no_cpu else cpu_baseline(pkg, args.cpu_threads)
 

@@ -103,6 +103,35 @@ const DeviceInfo &device_info() {
   return g_info[dev];
 }
 
+void *stream_workspace(hipStream_t s, size_t bytes) {
+  struct Entry {
+    int dev;
+    hipStream_t s;
+    void *p;
+    size_t bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  for (Entry &e : cache) {
+    if (e.dev != dev || e.s != s) continue;
+    if (e.bytes >= bytes) return e.p;
+    if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
+    (void)hipFree(e.p);
+    e.p = nullptr;
+    e.bytes = 0;
+    if (hipMalloc(&e.p, bytes) != hipSuccess) return e.p = nullptr;
+    e.bytes = bytes;
+    return e.p;
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+  cache.push_back(Entry{dev, s, p, bytes});
+  return p;
+}
+
 }  // namespace swamp
 
 using namespace swamp;

@@ -37,9 +37,11 @@
 //    its L2.
 //  * Decomposition: complete rounds of full tiles; a last round at most
 //    half full runs as twice as many 128-token half tiles (no partial
-//    sums); problems of at most half a round run as half tiles, and are
-//    split along K (pieces added into y with float atomics after zeroing)
-//    only when the half tiles still fill at most half the CUs.
+//    sums).  Problems of at most half a round split full tiles along K
+//    into up to 8 pieces whose partial tiles go to the stream's workspace
+//    and are summed in piece order by a second kernel (short K: half
+//    tiles; without a workspace: pieces added into zeroed y with float
+//    atomics).
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
 
@@ -316,6 +318,7 @@ __host__ __device__ inline void tile_coords(int t, int tiles_m, int tiles_n, int
 // each as `parts` token parts (1: full tile, 2: halves) x `splits` K pieces.
 struct Work {
   int tiles_m, tiles_n, first, parts, splits, kt_per_split;
+  float *part;  // splits > 1: partial sums [piece][M][N] (else added into y atomically)
 };
 
 template <int DT, int kTok>
@@ -435,8 +438,9 @@ __global__ void __launch_bounds__(kThreads, 1)
         const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * fc + (e & 3);
         if (m < M) {
           float *dst = y + size_t(m) * N + n;
-          if (atomic) unsafeAtomicAdd(dst, acc[i][e]);
-          else *dst = acc[i][e];
+          if (!atomic) *dst = acc[i][e];
+          else if (wk.part) wk.part[(size_t(piece) * M + m) * N + n] = acc[i][e];
+          else unsafeAtomicAdd(dst, acc[i][e]);
         }
       }
   }
@@ -456,6 +460,21 @@ __global__ void zero_tiles_kernel(float *__restrict__ y, int M, int N, int tiles
 #pragma unroll
   for (int i = 0; i < 4; i++)
     if (n + i < N) row[n + i] = 0.f;
+}
+
+// y = sum of the K pieces' partials, in piece order (deterministic); all
+// (at most 8) loads are issued before the adds.
+__global__ void split_reduce_kernel(const float *__restrict__ part, float *__restrict__ y,
+                                    int splits, size_t n) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v[8];
+#pragma unroll
+  for (int p = 0; p < 8; p++) v[p] = p < splits ? part[size_t(p) * n + i] : 0.f;
+  float s = v[0];
+#pragma unroll
+  for (int p = 1; p < 8; p++) s += v[p];  // missing pieces add 0
+  y[i] = s;
 }
 
 // ---- Q8_0 activation quantization ------------------------------------------
@@ -513,30 +532,70 @@ int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n, KT = n_cols / kBK;
   const int cus = swamp::device_info().num_cus;
-  // Full tiles in complete rounds; the rest as 128-token halves when they
-  // fill at most one round; K pieces when even the halves leave more than
-  // half the CUs idle (pieces at least 8 steps long).
-  int n_full = tiles, n_half = 0, splits = 1;
+  const size_t mn = size_t(m) * size_t(n_rows);
+  auto piece_len = [&](int splits) {  // K steps per piece (whole Q4_K blocks)
+    int kps = (KT + splits - 1) / splits;
+    if (DT == SWAMP_Q4_K) kps = (kps + 3) / 4 * 4;
+    return kps;
+  };
+  // At most half a round of tiles: either full tiles split along K into up
+  // to 8 pieces, or 128-token halves (split into up to 4 pieces when they
+  // fill at most half the CUs).  Split pieces write partial tiles to the
+  // stream's workspace, summed in piece order by a second kernel
+  // (deterministic); without a workspace, halves whose pieces add into
+  // zeroed y with float atomics.  The choice follows measured step times of
+  // one tile on one CU (full 2.0 us, half 1.3 us at 8B shapes) and 6 TB/s
+  // for the partial sums (written, read, y written).
+  if (2 * tiles <= cus) {
+    auto est_us = [&](double step_us, int pieces) {
+      double t_us = double(piece_len(pieces)) * step_us;
+      if (pieces > 1) t_us += (2.0 * pieces + 1.0) * double(mn) * 4.0 / 6e6;
+      return t_us;
+    };
+    int fs = std::min({cus / tiles, 8, KT / 8});
+    int hs = 4 * tiles <= cus ? std::max(1, std::min({cus / (2 * tiles), 4, KT / 8})) : 1;
+    const bool full = fs >= 2 && est_us(2.0, fs) < est_us(1.3, hs);
+    int pieces = full ? fs : hs;
+    const int kps = piece_len(pieces);
+    pieces = (KT + kps - 1) / kps;
+    float *part = nullptr;
+    if (pieces > 1)
+      part = static_cast<float *>(swamp::stream_workspace(s, size_t(pieces) * mn * sizeof(float)));
+    if (full && !part) {  // no workspace: halves instead
+      pieces = hs;
+      const int hk = piece_len(pieces);
+      pieces = (KT + hk - 1) / hk;
+    }
+    if (full && part) {
+      const Work wk{tiles_m, tiles_n, 0, 1, pieces, kps, part};
+      if (int rc = launch_tiles<DT, 8>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    } else {
+      const int hk = piece_len(pieces);
+      if (pieces > 1 && !part)
+        zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
+      const Work wk{tiles_m, tiles_n, 0, 2, pieces, hk, pieces > 1 ? part : nullptr};
+      if (int rc = launch_tiles<DT, 4>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    }
+    if (pieces > 1 && part) {
+      split_reduce_kernel<<<unsigned((mn + 255) / 256), 256, 0, s>>>(part, y, pieces, mn);
+      if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+    }
+    return SWAMP_OK;
+  }
+  // Full tiles in complete rounds; a last round at most half full as
+  // 128-token halves (twice the workgroups, no partial sums).
+  int n_half = 0;
   if (tiles >= cus) {
     const int rem = tiles % cus;
     if (rem > 0 && 2 * rem <= cus) n_half = rem;
-  } else if (2 * tiles <= cus) {
-    n_half = tiles;
-    if (4 * tiles <= cus) splits = std::max(1, std::min({cus / (2 * tiles), 4, KT / 8}));
   }
-  n_full = tiles - n_half;
-  int kt_per_split = (KT + splits - 1) / splits;
-  if (DT == SWAMP_Q4_K) kt_per_split = (kt_per_split + 3) / 4 * 4;  // whole blocks per piece
-  splits = (KT + kt_per_split - 1) / kt_per_split;
-  if (n_full > 0) {
-    const Work wk{tiles_m, tiles_n, 0, 1, 1, KT};
+  const int n_full = tiles - n_half;
+  {
+    const Work wk{tiles_m, tiles_n, 0, 1, 1, KT, nullptr};
     if (int rc = launch_tiles<DT, 8>(w, x, y, m, n_rows, n_cols, wk, n_full, s)) return rc;
   }
   if (n_half > 0) {
-    if (splits > 1)
-      zero_tiles_kernel<<<unsigned(n_half * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n,
-                                                              n_full);
-    const Work wk{tiles_m, tiles_n, n_full, 2, splits, kt_per_split};
+    const Work wk{tiles_m, tiles_n, n_full, 2, 1, KT, nullptr};
     if (int rc = launch_tiles<DT, 4>(w, x, y, m, n_rows, n_cols, wk, n_half, s)) return rc;
   }
   return SWAMP_OK;

@@ -30,7 +30,6 @@
 //    order (deterministic) after a barrier; nothing crosses workgroups.
 #include <cstdlib>
 #include <mutex>
-#include <vector>
 
 #include "swamp_common.hpp"
 #include "swamp_items.hpp"
@@ -638,40 +637,6 @@ int pass_kgroups(int n_tok, int n_rows, int n_cols) {
   return kg_plan(n_tok, n_rows, n_cols, pass_tok(n_tok)).nkg;
 }
 
-// The K groups' partial sums live in a workspace kept per (device,
-// stream): calls on one stream run in order, so they can share it, and
-// calls on different streams never do.  It grows when a larger one is
-// needed (after the stream's queued work has finished with the old one)
-// and is kept for the life of the process.
-float *stream_workspace(hipStream_t s, size_t bytes) {
-  struct Entry {
-    int dev;
-    hipStream_t s;
-    float *p;
-    size_t bytes;
-  };
-  static std::mutex mu;
-  static std::vector<Entry> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  for (Entry &e : cache) {
-    if (e.dev != dev || e.s != s) continue;
-    if (e.bytes >= bytes) return e.p;
-    if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
-    (void)hipFree(e.p);
-    e.p = nullptr;
-    e.bytes = 0;
-    if (hipMalloc(reinterpret_cast<void **>(&e.p), bytes) != hipSuccess) return e.p = nullptr;
-    e.bytes = bytes;
-    return e.p;
-  }
-  float *p = nullptr;
-  if (hipMalloc(reinterpret_cast<void **>(&p), bytes) != hipSuccess) return nullptr;
-  cache.push_back(Entry{dev, s, p, bytes});
-  return p;
-}
-
 template <int DT>
 int launch_pass(Args a, hipStream_t s) {
   if (a.n_tok <= 4) return launch_pass_tok<DT, 4>(a, s);
@@ -714,7 +679,7 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     if (nkg > 1) ws_bytes = std::max(ws_bytes, size_t(nkg) * nt * n_rows * sizeof(float));
   }
   // without a workspace the passes run as K phases
-  a.ws = ws_bytes ? stream_workspace(s, ws_bytes) : nullptr;
+  a.ws = ws_bytes ? static_cast<float *>(swamp::stream_workspace(s, ws_bytes)) : nullptr;
   int rc = SWAMP_OK;
   for (int t0 = 0; t0 < n_tok && rc == SWAMP_OK; t0 += kTok) {
     a.n_tok = std::min(kTok, n_tok - t0);

@@ -90,6 +90,14 @@ struct DeviceInfo {
 };
 const DeviceInfo &device_info();  // current device (initialises it)
 
+// Scratch memory of at least `bytes` for work queued on stream s of the
+// current device (partial sums of split reductions).  One buffer per
+// (device, stream): calls on one stream run in order and may share it,
+// calls on different streams never do.  It grows on demand (after the
+// stream's queued work is done with the old one) and lives until the
+// process exits.  nullptr when it cannot be allocated.
+void *stream_workspace(hipStream_t s, size_t bytes);
+
 }  // namespace swamp
 
 // Internal launchers (defined in dequant.hip, gemv.hip, gemv_fused.hip,

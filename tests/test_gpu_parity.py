@@ -377,8 +377,10 @@ def test_gemm_bf16_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
 # the CUs of one MI355X): complete rounds of full tiles; full tiles plus a
 # last round of 128-token half tiles (ragged tokens and rows: the second
 # half of the short last token tile is empty); one partial round of full
-# tiles; half tiles only, without a K split.
-DECOMP_CASES = [(2048, 8192, 4096), (1900, 28572, 4096), (2048, 6144, 4096), (2048, 4096, 14336)]
+# tiles; at most half a round: full tiles in 2 and in 5 K pieces summed
+# through the workspace; short K (8 steps): half tiles.
+DECOMP_CASES = [(2048, 8192, 4096), (1900, 28572, 4096), (2048, 6144, 4096), (2048, 4096, 14336),
+                (512, 6144, 4096), (100, 600, 512)]
 
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
@@ -398,7 +400,8 @@ def test_gemm_bf16_decompositions(pkg, orc, torch_dev, dtype, m, rows, cols):
     y = down(d_y)
     assert np.all(np.isfinite(y))
     # tokens at tile and half-tile edges, rows at both ends and the middle
-    toks = sorted(set([0, 127, 128, 255, 256, m // 2, m - 129, m - 128, m - 1]))
+    toks = sorted(set(k for k in [0, 127, 128, 255, 256, m // 2, m - 129, m - 128, m - 1]
+                      if 0 <= k < m))
     rb = pkg.row_bytes(dtype, cols)
     for r0, r1 in [(0, 384), (rows // 2 - 128, rows // 2 + 128), (rows - 300, rows)]:
         sub = raw[r0 * rb:r1 * rb]

@@ -40,7 +40,7 @@ namespace {
 using swamp::Raw;
 
 // Generic path for shapes the item kernel does not take (n_cols % 64 != 0
-// for Q4_0/Q8_0): one wavefront per row, one 32-weight block per lane step,
+// for Q4_0/Q8_0, or rows of more than 65536 weights): one wavefront per row, one 32-weight block per lane step,
 // byte loads.  Correct for any n_cols % 32 == 0.
 template <int DT>
 __global__ void __launch_bounds__(256) gemv_generic_kernel(const uint8_t *__restrict__ w,
@@ -112,16 +112,64 @@ __global__ void __launch_bounds__(256) gemv_generic_q6k_kernel(const uint8_t *__
   }
 }
 
+// Generic Q4_K path for rows longer than the item kernel takes (more than
+// 65536 weights): one wavefront per row, one 32-weight sub-block per lane
+// step, byte loads.  Sub-block j of a super-block uses qs[32 (j/2) ..],
+// low nibbles for even j, high for odd (layout A, q4_k.rs:290-319); its
+// 6-bit scale and min come unpacked as in q4_k.rs:37-53, and
+// sum((d sc) q - dmin m) x is taken as (d sc) sum(q x) - (dmin m) sum(x).
+__global__ void __launch_bounds__(256) gemv_generic_q4k_kernel(const uint8_t *__restrict__ w,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y, int n_rows,
+                                                               int n_cols) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nwaves = (gridDim.x * blockDim.x) >> 6;
+  const int nb = n_cols / 256;
+  for (int row = wave; row < n_rows; row += nwaves) {
+    const uint8_t *rp = w + size_t(row) * nb * 144;
+    float acc = 0.f;
+    for (int u = lane; u < nb * 8; u += 64) {
+      const int b = u >> 3, j = u & 7;
+      const uint8_t *blk = rp + size_t(b) * 144;
+      const float d = swamp::f16_bits_to_f32(uint32_t(blk[0]) | (uint32_t(blk[1]) << 8));
+      const float dmin = swamp::f16_bits_to_f32(uint32_t(blk[2]) | (uint32_t(blk[3]) << 8));
+      const uint8_t *sc = blk + 4;
+      uint32_t scale, mn;
+      if (j < 4) {
+        scale = sc[j] & 63u;
+        mn = sc[j + 4] & 63u;
+      } else {
+        scale = (sc[j + 4] & 0xFu) | ((uint32_t(sc[j - 4]) >> 6) << 4);
+        mn = (uint32_t(sc[j + 4]) >> 4) | ((uint32_t(sc[j]) >> 6) << 4);
+      }
+      const uint8_t *qs = blk + 16 + 32 * (j >> 1);
+      const int sh = 4 * (j & 1);
+      const float *xs = x + size_t(b) * 256 + 32 * j;
+      float sq = 0.f, sx = 0.f;
+      for (int i = 0; i < 32; i++) {
+        sq += float((uint32_t(qs[i]) >> sh) & 0xFu) * xs[i];
+        sx += xs[i];
+      }
+      acc += (d * float(scale)) * sq - (dmin * float(mn)) * sx;
+    }
+    acc = swamp::wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+  }
+}
+
 }  // namespace
 
 int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
                       int n_rows, int n_cols, hipStream_t s) {
   if (n_rows == 0) return SWAMP_OK;
   if (!item_path_ok(dtype, n_cols)) {
-    if (dtype == SWAMP_Q4_K) return SWAMP_ESHAPE;
     const int cus = swamp::device_info().num_cus;
     const int blocks = std::min((n_rows + 3) / 4, cus * 8);
-    if (dtype == SWAMP_Q6_K)
+    if (dtype == SWAMP_Q4_K)
+      gemv_generic_q4k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
+                                                     n_rows, n_cols);
+    else if (dtype == SWAMP_Q6_K)
       gemv_generic_q6k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
                                                      n_rows, n_cols);
     else if (dtype == SWAMP_Q4_0)

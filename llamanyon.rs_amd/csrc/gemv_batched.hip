@@ -246,16 +246,24 @@ struct Args {
   float *ws;       // nkg > 1: partial sums [nkg][n_tok][n_rows], reduced afterwards
 };
 
-// y[t][row0 + r] += / = v for the tokens and rows that exist; with K groups
-// the K group's partial sum goes to the workspace instead.
-__device__ __forceinline__ void put_y(const Args &a, int kg, int t, int row, float v) {
+// Output of a workgroup: y itself, or with K groups the K group's slice
+// of the workspace, which has y's layout [n_tok][n_rows]; partials are
+// stored, never accumulated.  One store path keeps the register count
+// under the 128 that 16 waves per CU allow.
+struct Out {
+  float *y;
+  int accumulate;
+};
+__device__ __forceinline__ Out out_of(const Args &a, int kg) {
+  if (a.nkg > 1) return {a.ws + size_t(kg) * a.n_tok * a.n_rows, 0};
+  return {a.y, a.accumulate};
+}
+
+// y[t][row] += / = v for the tokens and rows that exist.
+__device__ __forceinline__ void put_y(const Args &a, const Out &o, int t, int row, float v) {
   if (t < a.n_tok && row < a.n_rows) {
-    if (a.nkg > 1) {
-      a.ws[(size_t(kg) * a.n_tok + t) * a.n_rows + row] = v;
-    } else {
-      float *d = a.y + size_t(t) * a.n_rows + row;
-      *d = a.accumulate ? *d + v : v;
-    }
+    float *d = o.y + size_t(t) * a.n_rows + row;
+    *d = o.accumulate ? *d + v : v;
   }
 }
 
@@ -331,6 +339,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   // K group kg covers items [kg * ipk, kg * ipk + ipk) of its tiles
   const int G = gridDim.x / a.nkg, b = blockIdx.x % G, kg = blockIdx.x / G;
   const int kitem0 = kg * a.ipk;
+  const Out out = out_of(a, kg);
   const int J = (n_tg - 1 - b) / G + 1;  // tile groups of this workgroup (b < n_tg)
   const int cpw = a.ipw / (4 * kChunk);  // chunks per wave, tile and phase
   const int n_chunks = a.phases * cpw * J;
@@ -407,7 +416,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
     if (wk == 1) {
       if (tile < n_tiles) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) put_y(a, kg, 4 * g + i, tile * kRowsTile + r16, v[i]);
+        for (int i = 0; i < 4; i++) put_y(a, out, 4 * g + i, tile * kRowsTile + r16, v[i]);
       }
       return;
     }
@@ -421,7 +430,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       float sum = 0.f;
       for (int s2 = 0; s2 < wk; s2++) sum += src[s2 * 256];
       const int otile = (b + (batch * kJmax + k) * G) * wt + otl;
-      if (otile < n_tiles) put_y(a, kg, e >> 4, otile * kRowsTile + (e & 15), sum);
+      if (otile < n_tiles) put_y(a, out, e >> 4, otile * kRowsTile + (e & 15), sum);
     }
     lds_barrier();
   };

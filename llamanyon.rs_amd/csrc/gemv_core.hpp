@@ -674,13 +674,13 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
 }
 
 
-// Rows the item kernel takes: whole items, at most 2048 per row, and for
-// Q6_K an even number of blocks (4-byte aligned rows) and at most 1024
-// items (n_cols <= 65536).
+// Rows the item kernel takes: whole items, at most 1024 per row (n_cols <=
+// 65536: at most two items per lane, whose two register buffers fit without
+// spills), and for Q6_K an even number of blocks (4-byte aligned rows).
 bool item_path_ok(uint32_t dt, int n_cols) {
-  if (n_cols / 64 > 2048) return false;
+  if (n_cols / 64 > 1024) return false;
   if (dt == SWAMP_Q4_K) return true;
-  if (dt == SWAMP_Q6_K) return n_cols % 512 == 0 && n_cols / 64 <= 1024;
+  if (dt == SWAMP_Q6_K) return n_cols % 512 == 0;
   return n_cols % 64 == 0;
 }
 
@@ -771,14 +771,11 @@ int launch_rows(const MatSet &ms, const float *x, const Pro &pro, int n_cols, hi
   if (ipr <= 512) return launch_items<DT, 1, kRows, 8, kPro>(ms, x, pro, n_cols, s);
   // the fused prologues keep one item per lane (n_cols <= 32768)
   if constexpr (kPro != kProNone) return SWAMP_ESHAPE;
-  // With several items per lane the tiles are single rows (tile_rows_for
-  // caps them) so both register buffers fit without spills; a Q6_K item
-  // (19 dwords per row buffer) allows at most two items per lane, longer
-  // Q6_K rows take the generic kernel (item_path_ok).
+  // With two items per lane the tiles are single rows (tile_rows_for caps
+  // them) so both register buffers fit without spills; longer rows take
+  // the generic kernels (item_path_ok).
   else if constexpr (kRows > 1) return SWAMP_ESHAPE;
   else if (ipr <= 1024) return launch_items<DT, 2, 1, 8, kPro>(ms, x, pro, n_cols, s);
-  else if constexpr (DT == SWAMP_Q6_K) return SWAMP_ESHAPE;
-  else if (ipr <= 2048) return launch_items<DT, 4, 1, 8, kPro>(ms, x, pro, n_cols, s);
   return SWAMP_ESHAPE;
 }
 

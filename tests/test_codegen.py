@@ -8,7 +8,8 @@ tile's weight loads).  If the compiler ever issued another vector load in
 between, or turned one into a scalar load, the wait would release before the
 last DMA landed and a workgroup would read stale LDS -- wrong results that
 depend on timing.  This test compiles the two translation units to assembly
-and checks N against the loads actually emitted, for every instantiation."""
+and checks N against the loads actually emitted, for every instantiation.
+The same assembly shows whether any kernel spills registers to scratch."""
 import os
 import re
 import shutil
@@ -133,8 +134,41 @@ def _gemm_wait_problems(body):
     return probs
 
 
-def test_gemm_wait_counts_match_emitted_loads(tmp_path):
-    lines = _asm("gemm.hip", str(tmp_path / "gemm.s"))
+_TUS = ["api.hip", "dequant.hip", "gemv.hip", "gemv_fused.hip", "gemv_batched.hip", "gemm.hip",
+        "gemm_i8.hip", "gguf.hip"]
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    """Device assembly of every translation unit of the library, by name."""
+    d = tmp_path_factory.mktemp("asm")
+    with ThreadPoolExecutor(4) as ex:
+        return dict(zip(_TUS, ex.map(lambda t: _asm(t, str(d / (t + ".s"))), _TUS)))
+
+
+def test_no_kernel_uses_scratch(asm):
+    """Register spills go to scratch memory (per-lane HBM traffic on the hot
+    loops).  Every kernel of the library must fit its registers: the small
+    batch runs 16 waves per CU (128 VGPRs each), the GEMV up to 2 items per
+    lane."""
+    checked, bad = 0, []
+    for tu, lines in asm.items():
+        name = None
+        for line in lines:
+            m = re.match(r"^(_Z\w+):", line)
+            if m:
+                name = m.group(1)
+            m = re.match(r"^; ScratchSize: (\d+)", line)
+            if m and name:
+                checked += 1
+                if int(m.group(1)):
+                    bad.append((tu, name, int(m.group(1))))
+    assert checked >= 300, checked
+    assert not bad, bad
+
+
+def test_gemm_wait_counts_match_emitted_loads(asm):
+    lines = asm["gemm.hip"]
     kernels = list(_gemm_kernels(lines))
     # three weight formats x (full tile, half tile)
     assert len(kernels) == 6, [k for k, _ in kernels]
@@ -142,10 +176,9 @@ def test_gemm_wait_counts_match_emitted_loads(tmp_path):
     assert not bad, bad
 
 
-def test_staged_x_wait_counts_match_emitted_loads(tmp_path):
+def test_staged_x_wait_counts_match_emitted_loads(asm):
     tus = ["gemv.hip", "gemv_fused.hip"]
-    with ThreadPoolExecutor(2) as ex:
-        asms = list(ex.map(lambda t: _asm(t, str(tmp_path / (t + ".s"))), tus))
+    asms = [asm[t] for t in tus]
     checked, bad = 0, []
     for tu, lines in zip(tus, asms):
         for name, body in _kernels(lines):

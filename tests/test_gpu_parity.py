@@ -156,6 +156,13 @@ def test_gemv_parity(pkg, orc, torch_dev, dtype, rows, cols):
     _gemv_check(pkg, orc, torch_dev, dtype, rows, cols)
 
 
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("rows,cols", [(24, 65792), (9, 131072), (5, 262144)])
+def test_gemv_parity_long_rows(pkg, orc, torch_dev, dtype, rows, cols):
+    # rows of more than 65536 weights take the generic one-wave-per-row kernels
+    _gemv_check(pkg, orc, torch_dev, dtype, rows, cols)
+
+
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0])
 @pytest.mark.parametrize("cols", [64, 320, 96, 4064])
 def test_gemv_parity_small_blocks(pkg, orc, torch_dev, dtype, cols):

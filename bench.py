@@ -251,23 +251,26 @@ def run_sweep(pkg, torch, np, stream, lib):
                       "us": round(tot_us, 1), "GB/s": round(tot_b / tot_us / 1e3, 1),
                       "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
                       "matrices": per}), flush=True)
-    # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights
+    # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights (lm_head Q8_0)
     m = 4096
     per = []
-    for i, (name, rows, k) in enumerate(SWEEP_70B[:4]):
-        ws = weights_dev(pkg.Q4_K, rows, k, SEED ^ 0x500 ^ i, 0.015, 1)
+    for i, (name, rows, k) in enumerate(SWEEP_70B):
+        dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
+        ws = weights_dev(dt, rows, k, SEED ^ 0x500 ^ i, 0.015, 1)
         xb = torch.from_numpy(pkg.to_bf16_bits(
             pkg.fill_normal(SEED ^ 0x600 ^ i, 1.0, m, k)).view(np.int16)).cuda()
         y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
-        fn = lambda c: check(lib.swamp_qgemm(pkg.Q4_K, ws[0].data_ptr(), ws[0].numel(),
+        fn = lambda c: check(lib.swamp_qgemm(dt, ws[0].data_ptr(), ws[0].numel(),
                                              xb.data_ptr(), pkg.BF16, y.data_ptr(), m, rows, k,
                                              s), "swamp_qgemm")
         us = timed(fn, reps=5)
         tf = 2 * m * rows * k / us / 1e6
-        per.append({"name": name, "rows": rows, "k": k, "us": round(us, 1),
+        per.append({"name": name, "dtype": "Q8_0" if dt == pkg.Q8_0 else "Q4_K",
+                    "rows": rows, "k": k, "us": round(us, 1),
                     "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
         del ws, xb, y
-    print(json.dumps({"sweep": "llama3-70b prefill Q4_K x bf16, 4096 tokens", "matrices": per}),
+    print(json.dumps({"sweep": "llama3-70b prefill Q4_K (lm_head Q8_0) x bf16, 4096 tokens",
+                      "matrices": per}),
           flush=True)
 
 

@@ -13,8 +13,10 @@
 //    tile: 8 V_MFMA_F32_32X32X16_BF16 tiles, 128 fp32 accumulators.
 //  * Weights never touch LDS.  Each wave loads its own rows' items two K
 //    steps ahead and dequantizes them one step ahead straight into the
-//    B-operand layout (lane l: row 32w + l%32, k = 16s + 8(l/32) .. +7 of
-//    substep s), so every weight is converted once per tile.  With two
+//    B-operand layout (lane l: row 32w + l%32; for Q4_0 / Q8_0 weights
+//    32(l/32) + 8s .. +7 of the item in substep s, the activations read in
+//    the same k order, so a lane loads only the block it uses: 2 / 3 loads
+//    per step), and every weight is converted once per tile.  With two
 //    waves per SIMD, one wave's dequantization issues while the other's
 //    MFMAs run (vector ALU work issued by the wave that also issues the
 //    MFMAs stretches the MFMA cadence; another wave's does not).
@@ -50,7 +52,6 @@
 
 namespace {
 
-using swamp::Raw;
 using swamp::q4k_scales;
 using swamp::shr16;
 
@@ -72,7 +73,7 @@ struct Cfg {
   static constexpr int kXStage = kRows * kBK * 2;      // bytes of one stage
   static constexpr int kSmem = kStages * kXStage;      // 160 KB / 80 KB
   static constexpr int kDma = kRows * 128 / 1024 / kWaves;  // 1 KB DMAs per wave and step
-  static constexpr int kWLoads = DT == SWAMP_Q8_0 ? 5 : 3;  // weight loads per item
+  static constexpr int kWLoads = DT == SWAMP_Q4_0 ? 2 : 3;  // weight loads per item
   static constexpr int kVmem = kDma + kWLoads;         // vector-memory ops per step
 };
 
@@ -128,50 +129,77 @@ __device__ __forceinline__ u32x4v_t deq_bytes(uint32_t w0, uint32_t w1, float s,
   return out;
 }
 
-// B fragment of substep S for the lane's row: weights 16S + 8h .. +7 of
-// the item (h = lane / 32), i.e. 8-weight chunk c = 2S + h.  S is a
-// template argument so every index into the item is a constant: the item
-// array then lives in registers from the start, and a per-lane choice
-// between two of its words stays a register select.  Q = item % 4 (the
-// Q4_K quarter, whose sub-block scales the item uses) is one too, so the
-// scale unpacking has no branch.
+// Item weights (and activation k) that lane half h = lane / 32 supplies to
+// the MFMA of substep s, as the 8-weight chunk 0..7 of the K step.  Any
+// order works if A and B agree.  Q4_0 / Q8_0: chunk s + 4h, so a lane
+// needs weights 32h .. 32h + 31 only -- block h of the item (2 / 3 loads
+// instead of 3 / 5).  Q4_K: chunk 2s + h, so the sub-block (low nibbles
+// for s < 2, high for s >= 2) and its scale are constants of the substep;
+// the lane needs the whole quarter anyway.
+template <int DT>
+__host__ __device__ constexpr int k_chunk(int s, int h) {
+  return DT == SWAMP_Q4_K ? 2 * s + h : s + 4 * h;
+}
+
+// A lane's share of one weight item (64 weights of its row for one K
+// step): block h of a Q4_0 / Q8_0 item, loaded with the dword around its
+// start (block 1 starts 2 bytes into a dword); the whole Q4_K quarter.
+template <int DT>
+struct WItem;
+template <>
+struct WItem<SWAMP_Q4_0> {
+  uint32_t d[5];  // d[0]: item bytes 16..19; d[1..4]: bytes 0..15 (h = 0) or 20..35 (h = 1)
+};
+template <>
+struct WItem<SWAMP_Q8_0> {
+  uint32_t d[9];  // d[0]: item bytes 32..35; d[1..8]: bytes 0..31 (h = 0) or 36..67 (h = 1)
+};
+template <>
+struct WItem<SWAMP_Q4_K> {
+  uint32_t h[4];  // d, dmin, 12 scale bytes
+  uint32_t q[8];  // 32 nibble bytes of the quarter
+};
+
+// Per-lane byte offset (within the item) of the first 16-byte load.
+template <int DT>
+__host__ __device__ constexpr uint32_t half_offset(bool h) {
+  return !h ? 0u : DT == SWAMP_Q4_0 ? 20u : DT == SWAMP_Q8_0 ? 36u : 0u;
+}
+
+// B fragment of substep S for the lane's row: chunk k_chunk(S, h) of the
+// item.  S is a template argument so every index into the
+// item is a constant and the item stays in registers; the lane's half
+// only selects between two registers.  Q = item % 4 (the Q4_K quarter,
+// whose sub-block scales the item uses) is one too, so the scale
+// unpacking has no branch.
 template <int DT, int S, int Q>
-__device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, bool h) {
+__device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
   if constexpr (DT == SWAMP_Q4_0) {
-    // blocks at item bytes 0 and 18 (d, then 16 nibble bytes; byte b holds
-    // elements 2b and 2b + 1, q4_0.rs:30-35); chunk c's nibbles are bytes
-    // 4(c%4) .. +3 of its block: block 0's start 2 bytes into a dword
-    if constexpr (S < 2) {
-      constexpr int t = 2 * S;  // chunk 2S + h: dwords t + h and t + h + 1, shifted by 2 bytes
-      const uint32_t w = shr16(h ? r.d[t + 2] : r.d[t + 1], h ? r.d[t + 1] : r.d[t]);
-      const float d = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
-      return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
-    } else {
-      constexpr int t = 5 + 2 * (S - 2);
-      const uint32_t w = h ? r.d[t + 1] : r.d[t];
-      const float d = swamp::f16_bits_to_f32(r.d[4] >> 16);
-      return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
-    }
+    // block h: d, then 16 nibble bytes (byte b holds elements 2b and 2b + 1,
+    // q4_0.rs:30-35); chunk S is quant bytes 4S .. 4S + 3.  Block 0's quants
+    // start at byte 2 of d[1] (its bytes 16, 17 sit in d[0]); block 1's d is
+    // the high half of d[0] and its quants are d[1..4].
+    const uint32_t hi0 = S < 3 ? r.d[S + 2] : r.d[0];
+    const uint32_t w = h ? r.d[S + 1] : shr16(hi0, r.d[S + 1]);
+    const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
+    return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
   } else if constexpr (DT == SWAMP_Q8_0) {
-    // blocks at item bytes 0 and 34 (d, then 32 int8); chunk t = 2(S%2) + h
-    // of block S/2 is bytes 8t .. 8t+7 of its quants; bytes carry q + 128
-    // after the xor, value (q + 128) d - 128 d = q d exactly
-    if constexpr (S < 2) {
-      constexpr int t = 4 * S;  // chunk 2S starts at dword t (+2 bytes), 2S + 1 at t + 2
-      const uint32_t a = h ? r.d[t + 2] : r.d[t], b = h ? r.d[t + 3] : r.d[t + 1],
-                     c = h ? r.d[t + 4] : r.d[t + 2];
-      const float d = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
-      return deq_bytes(shr16(b, a) ^ 0x80808080u, shr16(c, b) ^ 0x80808080u, d, -128.0f * d);
-    } else {
-      constexpr int t = 9 + 4 * (S - 2);
-      const uint32_t w0 = h ? r.d[t + 2] : r.d[t], w1 = h ? r.d[t + 3] : r.d[t + 1];
-      const float d = swamp::f16_bits_to_f32(r.d[8] >> 16);
-      return deq_bytes(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, -128.0f * d);
-    }
+    // block h: d, then 32 int8; chunk S is quant bytes 8S .. 8S + 7.  Block
+    // 0's quants start at byte 2 of d[1] (bytes 32, 33 sit in d[0]); block
+    // 1's d is the high half of d[0] and its quants are d[1..8].  Bytes
+    // carry q + 128 after the xor: (q + 128) d - 128 d = q d exactly.
+    constexpr int j = 2 * S;
+    const uint32_t e2 = j + 2 < 9 ? r.d[j + 2] : r.d[0];
+    const uint32_t e3 = j + 3 < 9 ? r.d[j + 3] : r.d[0];
+    const uint32_t w0 = h ? r.d[j + 1] : shr16(e2, r.d[j + 1]);
+    const uint32_t w1 = h ? r.d[j + 2] : shr16(e3, e2);
+    const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
+    return deq_bytes(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, -128.0f * d);
   } else {
-    // Q4_K quarter: sub-block A = low nibbles of the 32 bytes (S < 2),
-    // sub-block B = high nibbles (S >= 2) (layout A, q4_k.rs:290-319);
-    // chunk 2(S%2) + h covers bytes 8(2(S%2) + h) .. +7
+    // Q4_K quarter, weights 16S + 8h .. +7: sub-block A = low nibbles of the
+    // 32 bytes (S < 2), sub-block B = high nibbles (S >= 2) (layout A,
+    // q4_k.rs:290-319); chunk 2(S%2) + h covers bytes 8(2(S%2) + h) .. +7.
+    // The sub-block, its mask and scale are constants of the substep.
     const float dd = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
@@ -186,37 +214,37 @@ __device__ __forceinline__ u32x4v_t b_frag(const Raw<DT> &r, bool h) {
   }
 }
 
-// Raw bytes of one weight item through a buffer resource: the lane's row in
-// the VGPR offset, the item's byte offset within a row in the (uniform) SGPR
-// offset.  Reads past the descriptor's range return zeros.
-
+// A lane's share of one weight item through a buffer resource: the lane's
+// row in the VGPR offset vrow (vhalf = vrow + half_offset), the item's byte
+// offset within a row in the (uniform) SGPR offset.  Reads past the
+// descriptor's range return zeros.
 template <int DT>
-__device__ __forceinline__ void load_item(Raw<DT> &r, __amdgpu_buffer_rsrc_t rs, uint32_t vrow,
-                                          int item) {
+__device__ __forceinline__ void load_item(WItem<DT> &r, __amdgpu_buffer_rsrc_t rs, uint32_t vrow,
+                                          uint32_t vhalf, int item) {
   if constexpr (DT == SWAMP_Q4_0) {
     const uint32_t so = uint32_t(item) * 36u;
-    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, so, 0);
-    const u32x4v_t b = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow + 16, so, 0);
+    r.d[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, vrow + 16, so, 0);
+    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vhalf, so, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) { r.d[i] = a[i]; r.d[4 + i] = b[i]; }
-    r.d[8] = __builtin_amdgcn_raw_buffer_load_b32(rs, vrow + 32, so, 0);
+    for (int i = 0; i < 4; i++) r.d[1 + i] = a[i];
   } else if constexpr (DT == SWAMP_Q8_0) {
     const uint32_t so = uint32_t(item) * 68u;
+    r.d[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, vrow + 32, so, 0);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow + 16 * j, so, 0);
+    for (int j = 0; j < 2; j++) {
+      const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vhalf + 16 * j, so, 0);
 #pragma unroll
-      for (int i = 0; i < 4; i++) r.d[4 * j + i] = a[i];
+      for (int i = 0; i < 4; i++) r.d[1 + 4 * j + i] = a[i];
     }
-    r.d[16] = __builtin_amdgcn_raw_buffer_load_b32(rs, vrow + 64, so, 0);
   } else {
+    (void)vhalf;
     const uint32_t hb = uint32_t(item >> 2) * 144u;
     const uint32_t so = hb + 16u + 32u * uint32_t(item & 3);
-    const u32x4v_t h = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, hb, 0);
+    const u32x4v_t hd = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, hb, 0);
     const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, so, 0);
     const u32x4v_t b = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow + 16, so, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) { r.h[i] = h[i]; r.q[i] = a[i]; r.q[4 + i] = b[i]; }
+    for (int i = 0; i < 4; i++) { r.h[i] = hd[i]; r.q[i] = a[i]; r.q[4 + i] = b[i]; }
   }
 }
 
@@ -231,6 +259,7 @@ struct Geo {
   uint32_t xs;     // m0 * K * 2 (scalar)
   uint32_t xinst;  // 8 * K * 2: scalar step between instructions
   uint32_t wv;     // per-lane weight row offset
+  uint32_t wvh;    // wv + half_offset (the lane's first 16-byte weight load)
   int wave;
 };
 
@@ -242,10 +271,12 @@ __device__ __forceinline__ void xdma(uint8_t *stage, const Geo &g, int kt) {
           g.xs + uint32_t(i) * g.xinst + uint32_t(kt) * 128u);
 }
 
-// A fragment of token tile i, substep ks (k = 16 ks + 8(l/32) .. +7).
+// A fragment of token tile i, substep ks: the 16-byte chunk
+// k_chunk(ks, l/32) of the token's row, the k order of b_frag.
+template <int DT>
 __device__ __forceinline__ bf16x8_t a_frag(const uint8_t *stg, int ks, int i, int lane) {
-  return *reinterpret_cast<const bf16x8_t *>(stg +
-                                             swz(32 * i + (lane & 31), 2 * ks + (lane >> 5)));
+  return *reinterpret_cast<const bf16x8_t *>(
+      stg + swz(32 * i + (lane & 31), k_chunk<DT>(ks, lane >> 5)));
 }
 
 // Substep KS of a K step (k = 16 KS .. 16 KS + 15): the MFMAs of every
@@ -258,18 +289,18 @@ template <int DT, int kTok, int KS, int Q>
 __device__ __forceinline__ void substep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
                                         const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
                                         const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
-                                        const Raw<DT> &nw, Raw<DT> &fetch, const Geo &g, int kt,
+                                        const WItem<DT> &nw, WItem<DT> &fetch, const Geo &g, int kt,
                                         int kt1, int lane) {
   using C = Cfg<DT, kTok>;
   if constexpr (KS == 0) {
     xdma<C::kDma>(dma, g, min(kt + kStages - 1, kt1 - 1));  // past the end: re-read
-    load_item<DT>(fetch, g.wr, g.wv, min(kt + 2, kt1 - 1));
+    load_item<DT>(fetch, g.wr, g.wv, g.wvh, min(kt + 2, kt1 - 1));
   }
 #pragma unroll
   for (int i = 0; i < kTok; i++) {
     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], __builtin_bit_cast(bf16x8_t, bc[KS]),
                                                      acc[i], 0, 0, 0);
-    a[i] = KS < 3 ? a_frag(cur, KS + 1, i, lane) : a_frag(nxt, 0, i, lane);
+    a[i] = KS < 3 ? a_frag<DT>(cur, KS + 1, i, lane) : a_frag<DT>(nxt, 0, i, lane);
   }
   bn[KS] = b_frag<DT, KS, Q>(nw, lane >= 32);
 #pragma unroll
@@ -291,7 +322,7 @@ template <int DT, int kTok, int Q>
 __device__ __forceinline__ void kstep(f32x16_t (&acc)[kTok], bf16x8_t (&a)[kTok],
                                       const uint8_t *cur, const uint8_t *nxt, uint8_t *dma,
                                       const u32x4v_t (&bc)[4], u32x4v_t (&bn)[4],
-                                      const Raw<DT> &nw, Raw<DT> &fetch, const Geo &g, int kt,
+                                      const WItem<DT> &nw, WItem<DT> &fetch, const Geo &g, int kt,
                                       int kt1, int lane) {
   using C = Cfg<DT, kTok>;
   substep<DT, kTok, 0, Q>(acc, a, cur, nxt, dma, bc, bn, nw, fetch, g, kt, kt1, lane);
@@ -366,6 +397,7 @@ __global__ void __launch_bounds__(kThreads, 1)
   const int nrows = min(kBN, N - n0);
   g.wr = swamp::make_rsrc(w + size_t(n0) * row_bytes, uint32_t(size_t(nrows) * row_bytes));
   g.wv = uint32_t(size_t(32 * wave + (lane & 31)) * row_bytes);
+  g.wvh = g.wv + half_offset<DT>(lane >= 32);
 
   f32x16_t acc[kTok];
 #pragma unroll
@@ -374,7 +406,7 @@ __global__ void __launch_bounds__(kThreads, 1)
     for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
 
   auto st = [&](int s) { return smem + C::kXStage * ((s - kt0) % kStages); };
-  Raw<DT> ra, rb;
+  WItem<DT> ra, rb;
   u32x4v_t ba[4], bb[4];
   bf16x8_t a[kTok];
   const bool h = lane >= 32;
@@ -386,11 +418,11 @@ __global__ void __launch_bounds__(kThreads, 1)
   __builtin_amdgcn_sched_barrier(0);
   xdma<C::kDma>(st(kt0 + 2), g, min(kt0 + 2, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
-  load_item<DT>(ra, g.wr, g.wv, kt0);
+  load_item<DT>(ra, g.wr, g.wv, g.wvh, kt0);
   __builtin_amdgcn_sched_barrier(0);
   xdma<C::kDma>(st(kt0 + 3), g, min(kt0 + 3, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
-  load_item<DT>(rb, g.wr, g.wv, min(kt0 + 1, kt1 - 1));
+  load_item<DT>(rb, g.wr, g.wv, g.wvh, min(kt0 + 1, kt1 - 1));
   __builtin_amdgcn_sched_barrier(0);
   ba[0] = b_frag<DT, 0, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
   ba[1] = b_frag<DT, 1, 0>(ra, h);  // kt0 % 4 == 0 for Q4_K
@@ -399,7 +431,7 @@ __global__ void __launch_bounds__(kThreads, 1)
   // x(kt0) and x(kt0+1) complete: 2 kVmem loads were issued after x(kt0+1)
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * C::kVmem) : "memory");
 #pragma unroll
-  for (int i = 0; i < kTok; i++) a[i] = a_frag(st(kt0), 0, i, lane);
+  for (int i = 0; i < kTok; i++) a[i] = a_frag<DT>(st(kt0), 0, i, lane);
 
   constexpr int D = kStages - 1;
   int kt = kt0;

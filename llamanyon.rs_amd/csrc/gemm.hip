@@ -13,10 +13,11 @@
 //    tile: 8 V_MFMA_F32_32X32X16_BF16 tiles, 128 fp32 accumulators.
 //  * Weights never touch LDS.  Each wave loads its own rows' items two K
 //    steps ahead and dequantizes them one step ahead straight into the
-//    B-operand layout (lane l: row 32w + l%32; for Q4_0 / Q8_0 weights
-//    32(l/32) + 8s .. +7 of the item in substep s, the activations read in
-//    the same k order, so a lane loads only the block it uses: 2 / 3 loads
-//    per step), and every weight is converted once per tile.  With two
+//    B-operand layout (lane l: row 32w + l%32, in a k order -- shared with
+//    the activation reads -- that lets a lane load only the part of the
+//    item it uses: one Q4_0 / Q8_0 block, half a Q4_K quarter with its
+//    header; 2, 3, 2 loads per step), and every weight is converted once
+//    per tile.  With two
 //    waves per SIMD, one wave's dequantization issues while the other's
 //    MFMAs run (vector ALU work issued by the wave that also issues the
 //    MFMAs stretches the MFMA cadence; another wave's does not).
@@ -73,7 +74,7 @@ struct Cfg {
   static constexpr int kXStage = kRows * kBK * 2;      // bytes of one stage
   static constexpr int kSmem = kStages * kXStage;      // 160 KB / 80 KB
   static constexpr int kDma = kRows * 128 / 1024 / kWaves;  // 1 KB DMAs per wave and step
-  static constexpr int kWLoads = DT == SWAMP_Q4_0 ? 2 : 3;  // weight loads per item
+  static constexpr int kWLoads = DT == SWAMP_Q8_0 ? 3 : 2;  // weight loads per item
   static constexpr int kVmem = kDma + kWLoads;         // vector-memory ops per step
 };
 
@@ -131,19 +132,21 @@ __device__ __forceinline__ u32x4v_t deq_bytes(uint32_t w0, uint32_t w1, float s,
 
 // Item weights (and activation k) that lane half h = lane / 32 supplies to
 // the MFMA of substep s, as the 8-weight chunk 0..7 of the K step.  Any
-// order works if A and B agree.  Q4_0 / Q8_0: chunk s + 4h, so a lane
-// needs weights 32h .. 32h + 31 only -- block h of the item (2 / 3 loads
-// instead of 3 / 5).  Q4_K: chunk 2s + h, so the sub-block (low nibbles
-// for s < 2, high for s >= 2) and its scale are constants of the substep;
-// the lane needs the whole quarter anyway.
+// order works if A and B agree; this one makes a lane need 36 B or less of
+// the item.  Q4_0 / Q8_0: chunk s + 4h, weights 32h .. 32h + 31 -- block h
+// of the item.  Q4_K: chunk 4(s/2) + 2h + s%2, i.e. low nibbles (sub-block
+// A) of quarter bytes 16h + 8(s%2) .. +7 for s < 2 and the high nibbles
+// (sub-block B) of the same bytes for s >= 2 -- 16 bytes of the quarter,
+// with the sub-block and its scale constants of the substep.
 template <int DT>
 __host__ __device__ constexpr int k_chunk(int s, int h) {
-  return DT == SWAMP_Q4_K ? 2 * s + h : s + 4 * h;
+  return DT == SWAMP_Q4_K ? 4 * (s >> 1) + 2 * h + (s & 1) : s + 4 * h;
 }
 
 // A lane's share of one weight item (64 weights of its row for one K
 // step): block h of a Q4_0 / Q8_0 item, loaded with the dword around its
-// start (block 1 starts 2 bytes into a dword); the whole Q4_K quarter.
+// start (block 1 starts 2 bytes into a dword); header and bytes 16h ..
+// 16h + 15 of a Q4_K quarter.
 template <int DT>
 struct WItem;
 template <>
@@ -157,13 +160,13 @@ struct WItem<SWAMP_Q8_0> {
 template <>
 struct WItem<SWAMP_Q4_K> {
   uint32_t h[4];  // d, dmin, 12 scale bytes
-  uint32_t q[8];  // 32 nibble bytes of the quarter
+  uint32_t q[4];  // nibble bytes 16h .. 16h + 15 of the quarter
 };
 
 // Per-lane byte offset (within the item) of the first 16-byte load.
 template <int DT>
 __host__ __device__ constexpr uint32_t half_offset(bool h) {
-  return !h ? 0u : DT == SWAMP_Q4_0 ? 20u : DT == SWAMP_Q8_0 ? 36u : 0u;
+  return !h ? 0u : DT == SWAMP_Q4_0 ? 20u : DT == SWAMP_Q8_0 ? 36u : 16u;
 }
 
 // B fragment of substep S for the lane's row: chunk k_chunk(S, h) of the
@@ -196,18 +199,19 @@ __device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
     const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
     return deq_bytes(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, -128.0f * d);
   } else {
-    // Q4_K quarter, weights 16S + 8h .. +7: sub-block A = low nibbles of the
-    // 32 bytes (S < 2), sub-block B = high nibbles (S >= 2) (layout A,
-    // q4_k.rs:290-319); chunk 2(S%2) + h covers bytes 8(2(S%2) + h) .. +7.
-    // The sub-block, its mask and scale are constants of the substep.
+    // Q4_K quarter: sub-block A = low nibbles of the 32 bytes (S < 2),
+    // sub-block B = high nibbles (S >= 2) (layout A, q4_k.rs:290-319), of
+    // the lane's bytes 8(S%2) .. +7.  The sub-block, its mask and scale are
+    // constants of the substep.
     const float dd = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
     q4k_scales(r.h, 2 * Q, sc0, m0, sc1, m1);  // Q: the item's quarter, a constant
     constexpr bool hb = S >= 2;
     const float sc = dd * float(hb ? sc1 : sc0), o = -(dmin * float(hb ? m1 : m0));
-    constexpr int t = 4 * (S & 1);
-    const uint32_t w0 = h ? r.q[t + 2] : r.q[t], w1 = h ? r.q[t + 3] : r.q[t + 1];
+    (void)h;
+    constexpr int t = 2 * (S & 1);
+    const uint32_t w0 = r.q[t], w1 = r.q[t + 1];
     // low nibbles: bytes of w & 0x0F0F0F0F; high: w & 0xF0F0F0F0 (16 q)
     constexpr uint32_t mask = hb ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
     return deq_bytes(w0 & mask, w1 & mask, hb ? 0.0625f * sc : sc, o);
@@ -237,14 +241,12 @@ __device__ __forceinline__ void load_item(WItem<DT> &r, __amdgpu_buffer_rsrc_t r
       for (int i = 0; i < 4; i++) r.d[1 + 4 * j + i] = a[i];
     }
   } else {
-    (void)vhalf;
     const uint32_t hb = uint32_t(item >> 2) * 144u;
     const uint32_t so = hb + 16u + 32u * uint32_t(item & 3);
     const u32x4v_t hd = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, hb, 0);
-    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow, so, 0);
-    const u32x4v_t b = __builtin_amdgcn_raw_buffer_load_b128(rs, vrow + 16, so, 0);
+    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(rs, vhalf, so, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) { r.h[i] = hd[i]; r.q[i] = a[i]; r.q[4 + i] = b[i]; }
+    for (int i = 0; i < 4; i++) { r.h[i] = hd[i]; r.q[i] = a[i]; }
   }
 }
 

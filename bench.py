@@ -383,7 +383,8 @@ def main():
 
     dom_name, dom_rows, dom_k = DECODE_SHAPES[dom]
     dom_bytes = alg_bytes_gemv(18, dom_rows, dom_k)
-    dom_us = float(np.mean([a.elapsed_ms(b) for a, b in ev])) * 1e3
+    dom_lat = np.array([a.elapsed_ms(b) for a, b in ev]) * 1e3
+    dom_us = float(np.mean(dom_lat))
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     traffic = traffic_from_profiles()
     roofline = {"bound": "hbm", "kernel": f"gemv_kernel<Q4_0> on {dom_name} "
@@ -391,7 +392,9 @@ def main():
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "alg_bytes_per_launch": dom_bytes,
-                "avg_launch_us": round(dom_us, 2)}
+                "avg_launch_us": round(dom_us, 2),
+                "launch_us_p10_p50_p90": [round(float(v), 2)
+                                          for v in np.percentile(dom_lat, [10, 50, 90])]}
 
     # ---- per-matrix kernel times (outside the timed region) --------------
     # Each matrix alone, 20 back-to-back launches over the rotated copies,

@@ -251,6 +251,36 @@ def run_sweep(pkg, torch, np, stream, lib):
                       "us": round(tot_us, 1), "GB/s": round(tot_b / tot_us / 1e3, 1),
                       "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
                       "matrices": per}), flush=True)
+    # activation producers of the 8B prefill at 2048 tokens: RMSNorm rows and
+    # SiLU(gate) * up, written as the GEMM's bf16 input
+    # (input copies rotate so that more than 512 MB cycles through the cache)
+    m, per = 2048, []
+    for name, k in (("rmsnorm_rows", 4096), ("swiglu", 14336)):
+        a0 = torch.from_numpy(pkg.fill_normal(SEED ^ 0x700, 1.0, m, k)).cuda()
+        b = torch.from_numpy(pkg.fill_normal(SEED ^ 0x701, 1.0, m, k)).cuda()
+        n_cp = max(3, -(-(512 << 20) // (m * k * 4)))
+        a = [a0] + [a0.clone() for _ in range(n_cp - 1)]
+        o = torch.empty((m, k), dtype=torch.int16, device="cuda")
+        if name == "rmsnorm_rows":
+            wn = b[0].contiguous()
+            fn = lambda c: check(lib.swamp_rmsnorm_rows(a[c % n_cp].data_ptr(), wn.data_ptr(),
+                                                        1e-5, o.data_ptr(), pkg.BF16, m, k, s),
+                                 "swamp_rmsnorm_rows")
+            nb = m * k * 4 + k * 4 + m * k * 2
+        else:
+            bl = [b] + [b.clone() for _ in range(n_cp - 1)]
+            fn = lambda c: check(lib.swamp_swiglu(a[c % n_cp].data_ptr(),
+                                                  bl[c % n_cp].data_ptr(), o.data_ptr(),
+                                                  pkg.BF16, m * k, s), "swamp_swiglu")
+            nb = 2 * m * k * 4 + m * k * 2
+        us = timed(fn)
+        per.append({"name": name, "m": m, "k": k, "us": round(us, 2), "bytes": nb,
+                    "GB/s": round(nb / us / 1e3, 1),
+                    "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+        a = b = bl = wn = None
+        del a0, o
+    print(json.dumps({"sweep": "llama3-8b prefill activation producers -> bf16, 2048 tokens",
+                      "kernels": per}), flush=True)
     # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights (lm_head Q8_0)
     m = 4096
     per = []

@@ -146,19 +146,40 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  * out [m][n_rows], OVERWRITTEN.  Replaces the prefill use of
  * forward_linear_batch (swamp-engine/src/executor.rs:106-110 ->
  * linear.rs:176-239).
- *   x_type SWAMP_BF16: d_x is bf16 [m][n_cols]; W is dequantized into LDS
- *     as bf16 and fed to bf16 MFMA (fp32 accumulate).
+ *   x_type SWAMP_BF16: d_x is bf16 [m][n_cols]; W is dequantized in
+ *     registers to bf16 and fed to bf16 MFMA (fp32 accumulate).
  *   x_type SWAMP_Q8_0: d_x is Q8_0 blocks [m][n_cols/32] (as produced by
  *     swamp_quantize_q8_0); int8 MFMA (one 32x32x32 instruction per
  *     32-weight block) against W's int8 codes (Q4_0: nibble - 8), each
  *     block's int32 result scaled by d_w * d_x into fp32.  Q4_0 and Q8_0
  *     weights only; n_cols a multiple of 128.
  * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only; Q6_K -> SWAMP_EDTYPE);
- * bf16 x needs n_cols a multiple of 64.  No workspace: when the tiles do not fill the GPU, K is
- * split across workgroups that add into y (zeroed by a fill kernel first). */
+ * bf16 x needs n_cols a multiple of 64.  When the tiles do not fill the
+ * GPU, K is split across workgroups whose partial tiles go to a scratch
+ * buffer the library keeps per (device, stream), summed in piece order by
+ * a second kernel (deterministic); calls on one stream share it. */
 int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);
+
+/* Activation producers for the small batch (out_type SWAMP_F32) and the
+ * prefill GEMM (SWAMP_BF16: its bf16 x, rounded to nearest even), over
+ * n_tok tokens in one pass.
+ * swamp_rmsnorm_rows: out[t] = (x[t] * inv) * w with inv = 1 /
+ *   sqrt(sum(x[t]^2) / n_cols + eps), d_x [n_tok][n_cols].  Replaces
+ *   rmsnorm (swamp-engine/src/ops.rs:188-201) before the QKV and FFN
+ *   projections (executor.rs:433, :488) for a whole batch or prompt.
+ * swamp_swiglu: out = silu(gate) * up = gate / (1 + exp(-gate)) * up over
+ *   n elements.  Replaces silu + mul_in_place (ops.rs:203-214) before the
+ *   down projection (executor.rs:501-502).
+ * Inputs 16-byte aligned, d_out 16-byte (fp32) or 8-byte (bf16) aligned;
+ * n_cols and n multiples of 4 (SWAMP_ESHAPE); out_type other than F32 /
+ * BF16: SWAMP_EDTYPE. */
+int swamp_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps,
+                       void *d_out, uint32_t out_type, int n_tok, int n_cols,
+                       void *stream);
+int swamp_swiglu(const float *d_gate, const float *d_up, void *d_out,
+                 uint32_t out_type, size_t n, void *stream);
 
 /* Activations to Q8_0 blocks on the device (the int8 GEMM's input):
  * x_type SWAMP_F32 or SWAMP_BF16, n a multiple of 32, d_q receives

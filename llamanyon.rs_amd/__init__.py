@@ -39,8 +39,8 @@ GPU_SYMBOLS = (
     "swamp_gpu_init", "swamp_strerror", "swamp_block_size", "swamp_type_size",
     "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_multi",
     "swamp_qgemv_rmsnorm", "swamp_qgemv_swiglu",
-    "swamp_qgemv_batched", "swamp_qgemm", "swamp_quantize_q8_0",
-    "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
+    "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
+    "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
 )
 # Every symbol include/swamp_gguf.h declares (also in libswamp_gpu.so).
 GGUF_SYMBOLS = (
@@ -105,6 +105,8 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_qgemv_swiglu": (i32, [u32, c_vp, c_size, c_vp, c_vp, c_vp, i32, i32, i32, c_vp]),
         "swamp_qgemv_batched": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, i32, i32, c_vp]),
         "swamp_qgemm": (i32, [u32, c_vp, c_size, c_vp, u32, c_vp, i32, i32, i32, c_vp]),
+        "swamp_rmsnorm_rows": (i32, [c_vp, c_vp, ctypes.c_float, c_vp, u32, i32, i32, c_vp]),
+        "swamp_swiglu": (i32, [c_vp, c_vp, c_vp, u32, c_size, c_vp]),
         "swamp_quantize_q8_0": (i32, [c_vp, u32, c_vp, c_size, c_vp]),
         "swamp_fused_gemv_q4k": (None, [c_vp, c_vp, c_vp, i32, i32]),
         "swamp_gemv_q8_vnni": (ctypes.c_float, [c_vp, c_vp, i32, ctypes.c_float]),
@@ -238,6 +240,18 @@ def qgemm(dtype: int, d_w: int, w_len: int, d_x: int, x_type: int, d_y: int, m: 
           n_rows: int, n_cols: int, stream: int = 0) -> None:
     _check(gpu_lib().swamp_qgemm(dtype, d_w, w_len, d_x, x_type, d_y, m, n_rows, n_cols, stream),
            "swamp_qgemm")
+
+
+def rmsnorm_rows(d_x: int, d_norm_w: int, eps: float, d_out: int, out_type: int, n_tok: int,
+                 n_cols: int, stream: int = 0) -> None:
+    """RMSNorm of n_tok rows (ops.rs:188-201) into fp32 or bf16 (the GEMM's x)."""
+    _check(gpu_lib().swamp_rmsnorm_rows(d_x, d_norm_w, eps, d_out, out_type, n_tok, n_cols,
+                                        stream), "swamp_rmsnorm_rows")
+
+
+def swiglu(d_gate: int, d_up: int, d_out: int, out_type: int, n: int, stream: int = 0) -> None:
+    """silu(gate) * up (ops.rs:203-214) into fp32 or bf16."""
+    _check(gpu_lib().swamp_swiglu(d_gate, d_up, d_out, out_type, n, stream), "swamp_swiglu")
 
 
 def quantize_q8_0(d_x: int, x_type: int, d_q: int, n: int, stream: int = 0) -> None:

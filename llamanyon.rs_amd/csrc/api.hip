@@ -325,6 +325,32 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
                            static_cast<hipStream_t>(stream));
 }
 
+int swamp_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps, void *d_out,
+                       uint32_t out_type, int n_tok, int n_cols, void *stream) {
+  if (out_type != SWAMP_F32 && out_type != SWAMP_BF16) return SWAMP_EDTYPE;
+  if (n_tok < 0 || n_cols < 0) return SWAMP_EINVAL;
+  if (n_cols % 4 != 0) return SWAMP_ESHAPE;
+  if (n_tok == 0 || n_cols == 0) return SWAMP_OK;
+  if (!d_x || !d_norm_w || !d_out || !aligned(d_x, 16) || !aligned(d_norm_w, 16) ||
+      !aligned(d_out, out_type == SWAMP_BF16 ? 8 : 16))
+    return SWAMP_EINVAL;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_rmsnorm_rows(d_x, d_norm_w, eps, d_out, out_type, n_tok, n_cols,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int swamp_swiglu(const float *d_gate, const float *d_up, void *d_out, uint32_t out_type, size_t n,
+                 void *stream) {
+  if (out_type != SWAMP_F32 && out_type != SWAMP_BF16) return SWAMP_EDTYPE;
+  if (n % 4 != 0) return SWAMP_ESHAPE;
+  if (n == 0) return SWAMP_OK;
+  if (!d_gate || !d_up || !d_out || !aligned(d_gate, 16) || !aligned(d_up, 16) ||
+      !aligned(d_out, out_type == SWAMP_BF16 ? 8 : 16))
+    return SWAMP_EINVAL;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_swiglu(d_gate, d_up, d_out, out_type, n, static_cast<hipStream_t>(stream));
+}
+
 int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n, void *stream) {
   if (x_type != SWAMP_F32 && x_type != SWAMP_BF16) return SWAMP_EDTYPE;
   if (n % 32 != 0) return SWAMP_ESHAPE;

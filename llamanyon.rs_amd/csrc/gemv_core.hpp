@@ -462,8 +462,6 @@ __device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
   }
 }
 
-// silu(g) * u = g / (1 + e^-g) * u with the hardware exp2 and reciprocal
-// (about 1 ulp each): g * rcp(1 + 2^(-g log2 e)) * u.
 // ---- x staged through LDS -------------------------------------------------
 // With one item per lane, a vector (x, or the prologue operand) reaches the
 // workgroup by direct-to-LDS DMA in 1 KB pieces (64 lanes x 16 B, adjacent
@@ -520,10 +518,7 @@ __device__ __forceinline__ void read_vec(float4 (&xv)[16], const uint8_t *lds, i
     xv[c] = *reinterpret_cast<const float4 *>(lds + 16 * (16 * item + (c ^ (item & 15))));
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
-}
+using swamp::silu_mul;
 
 // One workgroup = 64 * kWaves lanes; lane j owns items j, j + T, ...
 // (kPPT items per lane), covering one row of ipr items.  The workgroup

@@ -83,6 +83,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// silu(g) * u = g / (1 + e^-g) * u with the hardware exp2 and reciprocal
+// (about 1 ulp each): g * rcp(1 + 2^(-g log2 e)) * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 // Per-device properties cached by the host side.
 struct DeviceInfo {
   int device = -1;
@@ -101,7 +108,7 @@ void *stream_workspace(hipStream_t s, size_t bytes);
 }  // namespace swamp
 
 // Internal launchers (defined in dequant.hip, gemv.hip, gemv_fused.hip,
-// gemv_batched.hip, gemm.hip, gemm_i8.hip).  They
+// gemv_batched.hip, gemm.hip, gemm_i8.hip, producers.hip).  They
 // assume the arguments have been validated by api.cpp.
 int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
                          size_t n, hipStream_t s);
@@ -128,6 +135,10 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x,
                       int n_cols, hipStream_t s);
 int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, float *d_y, int m,
                          int n_rows, int n_cols, hipStream_t s);
+int swamp_launch_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps, void *d_out,
+                              uint32_t out_type, int n_tok, int n_cols, hipStream_t s);
+int swamp_launch_swiglu(const float *d_gate, const float *d_up, void *d_out, uint32_t out_type,
+                        size_t n, hipStream_t s);
 int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q,
                                size_t n, hipStream_t s);
 int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k,

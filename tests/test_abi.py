@@ -114,6 +114,18 @@ def test_argument_validation_precedes_device(pkg):
     assert sw(pkg.Q8_0, 4096, up=None) == pkg.EINVAL and sw(pkg.Q8_0, 4096, up=fake + 8) == pkg.EINVAL
     assert L.swamp_qdequant(pkg.Q4_0, fake, 35, fake, 64, None) == pkg.ESHAPE
     assert L.swamp_quantize_q8_0(fake, pkg.F32, fake, 33, None) == pkg.ESHAPE
+    # activation producers: argument errors return before any device work
+    rr = lambda ot, t, c, x=fake, w=fake, o=fake: L.swamp_rmsnorm_rows(x, w, 1e-5, o, ot, t, c,
+                                                                       None)
+    assert rr(pkg.F32, 4, 4098) == pkg.ESHAPE and rr(pkg.Q8_0, 4, 4096) == pkg.EDTYPE
+    assert rr(pkg.F32, -1, 4096) == pkg.EINVAL and rr(pkg.F32, 4, -4) == pkg.EINVAL
+    assert rr(pkg.F32, 4, 4096, x=None) == pkg.EINVAL and rr(pkg.F32, 4, 4096, w=fake + 4) == pkg.EINVAL
+    assert rr(pkg.F32, 4, 4096, o=fake + 8) == pkg.EINVAL and rr(pkg.BF16, 4, 4096, o=fake + 4) == pkg.EINVAL
+    assert rr(pkg.F32, 0, 4096) == pkg.OK and rr(pkg.BF16, 4, 0, x=None) == pkg.OK
+    sg = lambda ot, n, g=fake, u=fake, o=fake: L.swamp_swiglu(g, u, o, ot, n, None)
+    assert sg(pkg.F32, 14338) == pkg.ESHAPE and sg(pkg.F16, 14336) == pkg.EDTYPE
+    assert sg(pkg.BF16, 14336, u=None) == pkg.EINVAL and sg(pkg.F32, 14336, g=fake + 4) == pkg.EINVAL
+    assert sg(pkg.BF16, 14336, o=fake + 2) == pkg.EINVAL and sg(pkg.F32, 0, g=None) == pkg.OK
     n = 9
     dts = (ctypes.c_uint32 * n)(*([pkg.Q4_0] * n))
     assert L.swamp_qgemv_multi(n, dts, None, None, None, fake, None, 64, None) == pkg.EINVAL

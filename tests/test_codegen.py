@@ -135,7 +135,7 @@ def _gemm_wait_problems(body):
 
 
 _TUS = ["api.hip", "dequant.hip", "gemv.hip", "gemv_fused.hip", "gemv_batched.hip", "gemm.hip",
-        "gemm_i8.hip", "gguf.hip"]
+        "gemm_i8.hip", "gguf.hip", "producers.hip"]
 
 
 @pytest.fixture(scope="module")

@@ -6,9 +6,10 @@
 // Replaces, for a whole prompt or batch, the per-token rmsnorm before the
 // QKV and FFN projections (swamp-engine/src/executor.rs:433, :488) and the
 // silu + mul_in_place before the down projection (:501-502).  HBM-bound
-// single passes: RMSNorm reads x twice (the second read of a row hits the
-// cache) and w, SwiGLU reads gate and up once; each writes its output once,
-// so the GEMM gets its bf16 input without a separate cast.
+// single passes: RMSNorm reads x (kept in registers between the sum of
+// squares and the scaling) and w, SwiGLU reads gate and up once; each
+// writes its output once, so the GEMM gets its bf16 input without a
+// separate cast.
 //
 // Arithmetic: inv_rms = rsq(sum(x^2) / n + eps) and out = (x * inv_rms) * w
 // as in the fused decode GEMV's prologue; silu(g) * u = g * rcp(1 + 2^(-g
@@ -37,7 +38,11 @@ __device__ __forceinline__ void store4(__bf16 *o, size_t i, float4 v) {
 
 constexpr int kThreads = 256;
 
-// One workgroup per token row; n_cols % 4 == 0, rows 16-byte aligned.
+// One workgroup per token row; n_cols % 4 == 0, rows 16-byte aligned.  The
+// first kKeep float4 of each thread (rows up to 8192 floats) stay in
+// registers between the sum of squares and the scaling; longer rows read
+// the rest again.
+constexpr int kKeep = 8;
 template <typename OutT>
 __global__ void __launch_bounds__(kThreads) rmsnorm_rows_kernel(const float *__restrict__ x,
                                                                 const float *__restrict__ w,
@@ -45,8 +50,19 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_rows_kernel(const float *__r
                                                                 int n_cols) {
   const size_t row = size_t(blockIdx.x) * size_t(n_cols);
   const float *xr = x + row;
+  const int i0 = 4 * int(threadIdx.x);
+  float4 keep[kKeep];
+#pragma unroll
+  for (int j = 0; j < kKeep; j++) {
+    const int i = i0 + 4 * kThreads * j;
+    keep[j] = i < n_cols ? *reinterpret_cast<const float4 *>(xr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   float ss = 0.f;
-  for (int i = 4 * int(threadIdx.x); i < n_cols; i += 4 * kThreads) {
+#pragma unroll
+  for (int j = 0; j < kKeep; j++)
+    ss += keep[j].x * keep[j].x + keep[j].y * keep[j].y + keep[j].z * keep[j].z +
+          keep[j].w * keep[j].w;
+  for (int i = i0 + 4 * kThreads * kKeep; i < n_cols; i += 4 * kThreads) {
     const float4 v = *reinterpret_cast<const float4 *>(xr + i);
     ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
@@ -58,12 +74,18 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_rows_kernel(const float *__r
 #pragma unroll
   for (int k = 0; k < kThreads / 64; k++) tot += part[k];
   const float inv = __builtin_amdgcn_rsqf(tot / float(n_cols) + eps);
-  for (int i = 4 * int(threadIdx.x); i < n_cols; i += 4 * kThreads) {
-    const float4 v = *reinterpret_cast<const float4 *>(xr + i);
+  auto put = [&](int i, float4 v) {
     const float4 g = *reinterpret_cast<const float4 *>(w + i);
     store4(out, row + size_t(i),
            make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w));
+  };
+#pragma unroll
+  for (int j = 0; j < kKeep; j++) {
+    const int i = i0 + 4 * kThreads * j;
+    if (i < n_cols) put(i, keep[j]);
   }
+  for (int i = i0 + 4 * kThreads * kKeep; i < n_cols; i += 4 * kThreads)
+    put(i, *reinterpret_cast<const float4 *>(xr + i));
 }
 
 // Grid-stride over n4 groups of 4 elements.

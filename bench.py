@@ -27,11 +27,12 @@ Also reported (outside the timed steps):
     dot), restated in C, timed on this host's cores on one step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--no-prefill] [--cpu-threads T] [--sweep] [--pmc-probe]
+                       [--no-prefill] [--cpu-threads T] [--sweep] [--pmc-probe] [--pmc-gemm]
 --sweep adds one JSON line per extra workload after the main line: the
 Q4_K small-batch sweep (1/4/8/16 tokens) at 8B shapes and the 70B layer
 (decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
-and a copy of known size, for the rocprofv3 --pmc traffic measurement.
+and a copy of known size, for the rocprofv3 --pmc traffic measurement;
+--pmc-gemm the same for the 2048-token gate+up prefill GEMM.
 """
 from __future__ import annotations
 
@@ -317,6 +318,9 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also print one line per extra workload (8B small-batch Q4_K sweep, "
                          "70B decode and prefill) after the main line")
+    ap.add_argument("--pmc-gemm", action="store_true",
+                    help="only run 5 calls of the 2048-token gate+up prefill GEMM (Q4_0 x bf16) "
+                         "and one 256 MiB device copy (for rocprofv3 --pmc), no JSON")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
@@ -353,6 +357,31 @@ def main():
     step_bytes = sum(alg_bytes_gemv(18, r, k) for _, r, k in DECODE_SHAPES)
     rotated = sum(t.numel() for st in sets for t in st)
     lib = pkg.gpu_lib()
+
+    if args.pmc_gemm:
+        # the prefill GEMM under rocprofv3 --pmc: 5 calls of the 2048-token
+        # gate+up (each a full-tile and a half-tile launch), then the same
+        # calibration copy as --pmc-probe
+        name, rows, k = PREFILL_SHAPES[0]
+        pm = PREFILL_MS[0]
+        raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x100, 0.02, rows, k)
+        w = torch.from_numpy(raw).cuda()
+        xg = torch.from_numpy(pkg.to_bf16_bits(pkg.fill_normal(SEED ^ 0x200, 1.0, pm, k))
+                              .view(np.int16)).cuda()
+        yg = torch.empty((pm, rows), dtype=torch.float32, device="cuda")
+        for _ in range(5):
+            rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xg.data_ptr(), pkg.BF16,
+                                 yg.data_ptr(), pm, rows, k, s)
+            if rc != 0:
+                raise pkg.GpuError(rc, "swamp_qgemm")
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"pmc gemm: 5 x swamp_qgemm Q4_0 {name} {pm}x{rows}x{k} (bf16 x), then a "
+              f"{src.numel()}-byte device copy", flush=True)
+        return
 
     if args.pmc_probe:
         # HBM traffic of the dominant kernel under rocprofv3 --pmc: its

@@ -177,13 +177,16 @@ __host__ __device__ constexpr uint32_t half_offset(bool h) {
 // unpacking has no branch.
 template <int DT, int S, int Q>
 __device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
+  // block 0's quants start 2 bytes into their dwords, block 1's on a dword:
+  // one byte-align per dword with a per-lane shift (2 or 0) serves both
+  const uint32_t sh = h ? 0u : 2u;
   if constexpr (DT == SWAMP_Q4_0) {
     // block h: d, then 16 nibble bytes (byte b holds elements 2b and 2b + 1,
     // q4_0.rs:30-35); chunk S is quant bytes 4S .. 4S + 3.  Block 0's quants
     // start at byte 2 of d[1] (its bytes 16, 17 sit in d[0]); block 1's d is
     // the high half of d[0] and its quants are d[1..4].
     const uint32_t hi0 = S < 3 ? r.d[S + 2] : r.d[0];
-    const uint32_t w = h ? r.d[S + 1] : shr16(hi0, r.d[S + 1]);
+    const uint32_t w = __builtin_amdgcn_alignbyte(hi0, r.d[S + 1], sh);
     const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
     return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
   } else if constexpr (DT == SWAMP_Q8_0) {
@@ -194,11 +197,12 @@ __device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
     constexpr int j = 2 * S;
     const uint32_t e2 = j + 2 < 9 ? r.d[j + 2] : r.d[0];
     const uint32_t e3 = j + 3 < 9 ? r.d[j + 3] : r.d[0];
-    const uint32_t w0 = h ? r.d[j + 1] : shr16(e2, r.d[j + 1]);
-    const uint32_t w1 = h ? r.d[j + 2] : shr16(e3, e2);
+    const uint32_t w0 = __builtin_amdgcn_alignbyte(e2, r.d[j + 1], sh);
+    const uint32_t w1 = __builtin_amdgcn_alignbyte(e3, e2, sh);
     const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
     return deq_bytes(w0 ^ 0x80808080u, w1 ^ 0x80808080u, d, -128.0f * d);
   } else {
+    (void)sh;
     // Q4_K quarter: sub-block A = low nibbles of the 32 bytes (S < 2),
     // sub-block B = high nibbles (S >= 2) (layout A, q4_k.rs:290-319), of
     // the lane's bytes 8(S%2) .. +7.  The sub-block, its mask and scale are

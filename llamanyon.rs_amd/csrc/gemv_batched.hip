@@ -694,6 +694,12 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     a.n_tok = std::min(kTok, n_tok - t0);
     a.x = d_x + size_t(t0) * n_cols;
     a.y = d_y + size_t(t0) * n_rows;
+    // a pass of one token written over y is a GEMV: the one-token kernel
+    // streams the weights faster (8B Q4_K gate+up 15 us against 21 us here)
+    if (a.n_tok == 1 && !accumulate) {
+      rc = swamp_launch_gemv(dtype, d_w, a.x, a.y, n_rows, n_cols, s);
+      continue;
+    }
     switch (dtype) {
     case SWAMP_Q4_0: rc = launch_pass<SWAMP_Q4_0>(a, s); break;
     case SWAMP_Q8_0: rc = launch_pass<SWAMP_Q8_0>(a, s); break;

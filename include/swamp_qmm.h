@@ -134,7 +134,10 @@ int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * fused_gemv_q4k_batched, fused_gemv_q4k.rs:527-554, :694).
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
- * 16 tokens (Q4_0, Q8_0, Q4_K).  Q6_K: forward_linear_batch sends it to
+ * 16 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass of one token
+ * runs the decode GEMV, and n_tok > 32 runs swamp_qgemm's kernels on x
+ * rounded to bf16 (kept in a per-(device, stream) buffer the library
+ * allocates on first use).  Q6_K: forward_linear_batch sends it to
  * fallback_gemv (linear.rs:336-364), the GEMV per token written over y;
  * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
  * SWAMP_EDTYPE. */

@@ -103,10 +103,11 @@ const DeviceInfo &device_info() {
   return g_info[dev];
 }
 
-void *stream_workspace(hipStream_t s, size_t bytes) {
+void *stream_workspace(hipStream_t s, size_t bytes, int slot) {
   struct Entry {
     int dev;
     hipStream_t s;
+    int slot;
     void *p;
     size_t bytes;
   };
@@ -116,7 +117,7 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
   for (Entry &e : cache) {
-    if (e.dev != dev || e.s != s) continue;
+    if (e.dev != dev || e.s != s || e.slot != slot) continue;
     if (e.bytes >= bytes) return e.p;
     if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
     (void)hipFree(e.p);
@@ -128,7 +129,7 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
   }
   void *p = nullptr;
   if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-  cache.push_back(Entry{dev, s, p, bytes});
+  cache.push_back(Entry{dev, s, slot, p, bytes});
   return p;
 }
 

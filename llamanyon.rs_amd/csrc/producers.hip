@@ -103,7 +103,27 @@ __global__ void __launch_bounds__(kThreads) swiglu_kernel(const float *__restric
   }
 }
 
+// fp32 -> bf16 (round to nearest even), grid-stride over n4 groups of 4.
+__global__ void __launch_bounds__(kThreads) f32_to_bf16_kernel(const float *__restrict__ x,
+                                                               __bf16 *__restrict__ out,
+                                                               size_t n4) {
+  for (size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x; i < n4;
+       i += size_t(gridDim.x) * kThreads)
+    store4(out, 4 * i, reinterpret_cast<const float4 *>(x)[i]);
+}
+
+unsigned stream_grid(size_t n4) {
+  const size_t want = (n4 + kThreads - 1) / kThreads;
+  return unsigned(std::min<size_t>(want, size_t(swamp::device_info().num_cus) * 16));
+}
+
 }  // namespace
+
+int swamp_launch_f32_to_bf16(const float *d_x, void *d_out, size_t n, hipStream_t s) {
+  f32_to_bf16_kernel<<<stream_grid(n / 4), kThreads, 0, s>>>(d_x, static_cast<__bf16 *>(d_out),
+                                                             n / 4);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
 
 int swamp_launch_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps, void *d_out,
                               uint32_t out_type, int n_tok, int n_cols, hipStream_t s) {
@@ -119,9 +139,7 @@ int swamp_launch_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps
 int swamp_launch_swiglu(const float *d_gate, const float *d_up, void *d_out, uint32_t out_type,
                         size_t n, hipStream_t s) {
   const size_t n4 = n / 4;
-  const size_t want = (n4 + kThreads - 1) / kThreads;
-  const unsigned grid =
-      unsigned(std::min<size_t>(want, size_t(swamp::device_info().num_cus) * 16));
+  const unsigned grid = stream_grid(n4);
   if (out_type == SWAMP_BF16)
     swiglu_kernel<__bf16><<<grid, kThreads, 0, s>>>(d_gate, d_up, static_cast<__bf16 *>(d_out), n4);
   else

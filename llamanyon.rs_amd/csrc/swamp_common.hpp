@@ -98,12 +98,14 @@ struct DeviceInfo {
 const DeviceInfo &device_info();  // current device (initialises it)
 
 // Scratch memory of at least `bytes` for work queued on stream s of the
-// current device (partial sums of split reductions).  One buffer per
-// (device, stream): calls on one stream run in order and may share it,
-// calls on different streams never do.  It grows on demand (after the
-// stream's queued work is done with the old one) and lives until the
-// process exits.  nullptr when it cannot be allocated.
-void *stream_workspace(hipStream_t s, size_t bytes);
+// current device.  One buffer per (device, stream, slot): calls on one
+// stream run in order and may share it, calls on different streams never
+// do; slot 0 holds partial sums of split reductions, slot 1 converted
+// activations (which a call may hold while it uses slot 0).  A buffer
+// grows on demand (after the stream's queued work is done with the old
+// one) and lives until the process exits.  nullptr when it cannot be
+// allocated.
+void *stream_workspace(hipStream_t s, size_t bytes, int slot = 0);
 
 }  // namespace swamp
 
@@ -139,6 +141,7 @@ int swamp_launch_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps
                               uint32_t out_type, int n_tok, int n_cols, hipStream_t s);
 int swamp_launch_swiglu(const float *d_gate, const float *d_up, void *d_out, uint32_t out_type,
                         size_t n, hipStream_t s);
+int swamp_launch_f32_to_bf16(const float *d_x, void *d_out, size_t n, hipStream_t s);
 int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q,
                                size_t n, hipStream_t s);
 int swamp_launch_i8dot(const int8_t *d_w, const int8_t *d_a, int k,

@@ -231,9 +231,10 @@ def test_gemv_multi(pkg, orc, torch_dev):
 # ------------------------------------------------------------ small batch
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
-@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19])
+@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19, 33, 70])
 @pytest.mark.parametrize("rows,cols", [(1000, 4096), (256, 14336)])
 def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
+    # 1 token: the decode GEMV; 33 and 70: the prefill GEMM on bf16-rounded x
     torch = torch_dev
     raw = weights(pkg, dtype, rows, cols, mid=n_tok)
     xs = acts(pkg, n_tok, cols, mid=n_tok)
@@ -337,11 +338,13 @@ def test_batched_two_streams(pkg, torch_dev):
 
 
 @pytest.mark.parametrize("cols", [4096, 14336])
-def test_batched_accumulate(pkg, orc, torch_dev, cols):
+@pytest.mark.parametrize("n_tok", [1, 6, 40])
+def test_batched_accumulate(pkg, orc, torch_dev, cols, n_tok):
     """accumulate=1 is the kernel contract of fused_gemv_q4k_batched
-    (out += W x, fused_gemv_q4k.rs:694)."""
+    (out += W x, fused_gemv_q4k.rs:694); it keeps every pass, of one token
+    or of more than 32, on the small-batch kernel."""
     torch = torch_dev
-    rows, n_tok = 512, 6
+    rows = 512
     raw = weights(pkg, Q4_K, rows, cols, mid=3)
     xs = acts(pkg, n_tok, cols, mid=3)
     base = np.random.default_rng(1).standard_normal((n_tok, rows)).astype(np.float32)

@@ -137,8 +137,10 @@ int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * 16 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass of one token
  * runs the decode GEMV, and n_tok > 32 runs swamp_qgemm's kernels on x
  * rounded to bf16 (kept in a per-(device, stream) buffer the library
- * allocates on first use).  Q6_K: forward_linear_batch sends it to
- * fallback_gemv (linear.rs:336-364), the GEMV per token written over y;
+ * allocates on first use).  The 2..32-token kernel rounds x to fp16:
+ * entries must lie within its range (|x| < 65504).  Q6_K:
+ * forward_linear_batch sends it to fallback_gemv (linear.rs:336-364), the
+ * GEMV per token written over y;
  * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
  * SWAMP_EDTYPE. */
 int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,

@@ -135,9 +135,9 @@ int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
  * 16 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass of one token
- * runs the decode GEMV, and n_tok > 32 runs swamp_qgemm's kernels on x
+ * runs the decode GEMV, and n_tok > 16 runs swamp_qgemm's kernels on x
  * rounded to bf16 (kept in a per-(device, stream) buffer the library
- * allocates on first use).  The 2..32-token kernel rounds x to fp16:
+ * allocates on first use).  The 2..16-token kernel rounds x to fp16:
  * entries must lie within its range (|x| < 65504).  Q6_K:
  * forward_linear_batch sends it to fallback_gemv (linear.rs:336-364), the
  * GEMV per token written over y;

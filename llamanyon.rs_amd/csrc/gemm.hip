@@ -38,7 +38,9 @@
 //    (ids i, i+8, ...) runs a contiguous run of that order.  A round of an
 //    XCD's 32 CUs then shares 4 activation slabs and 8 weight columns in
 //    its L2.
-//  * Decomposition: complete rounds of full tiles; a last round at most
+//  * Decomposition: at most 64 tokens run as 64-token tiles (a quarter of
+//    the MFMA work per weight stream), split along K while they fill at
+//    most half the CUs.  Otherwise complete rounds of full tiles; a last round at most
 //    half full runs as twice as many 128-token half tiles (no partial
 //    sums).  Problems of at most half a round split full tiles along K
 //    into up to 8 pieces whose partial tiles go to the stream's workspace
@@ -257,8 +259,8 @@ __device__ __forceinline__ void load_item(WItem<DT> &r, __amdgpu_buffer_rsrc_t r
 // Per-lane load geometry.  DMA instruction i of wave w fills stage bytes
 // [1024 (kDma w + i), +1024) = tile rows 8(kDma w + i) .. +7: lane L writes
 // row 8(kDma w + i) + L/8, physical chunk L%8, and fetches the logical chunk
-// the swizzle puts there, (L%8) ^ ((row / 2) % 8) = (L%8) ^ ((4i + L/16) % 8)
-// (kDma w is even).  The weight item of the lane is row 32w + L%32.
+// the swizzle puts there, (L%8) ^ ((row / 2) % 8) = (L%8) ^ ((4p + L/16) % 8)
+// with p = (kDma w + i) % 2: xv[p].  The weight item of the lane is row 32w + L%32.
 struct Geo {
   __amdgpu_buffer_rsrc_t xr, wr;
   uint32_t xv[2];  // per-lane DMA offsets for even / odd instructions
@@ -272,8 +274,8 @@ struct Geo {
 template <int kDma>
 __device__ __forceinline__ void xdma(uint8_t *stage, const Geo &g, int kt) {
 #pragma unroll
-  for (int i = 0; i < kDma; i++)
-    dma16(g.xr, stage + 1024 * (kDma * g.wave + i), g.xv[i & 1],
+  for (int i = 0; i < kDma; i++)  // the swizzle of rows 8(kDma w + i) .. +7 has parity kDma w + i
+    dma16(g.xr, stage + 1024 * (kDma * g.wave + i), ((kDma * g.wave + i) & 1) ? g.xv[1] : g.xv[0],
           g.xs + uint32_t(i) * g.xinst + uint32_t(kt) * 128u);
 }
 
@@ -584,6 +586,26 @@ int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows
   // zeroed y with float atomics.  The choice follows measured step times of
   // one tile on one CU (full 2.0 us, half 1.3 us at 8B shapes) and 6 TB/s
   // for the partial sums (written, read, y written).
+  // At most 64 tokens: 64-token tiles (a quarter of the MFMA work of a
+  // full tile for the same weight stream), split along K while they fill
+  // at most half the CUs.
+  if (m <= kBM / 4) {
+    int pieces = 2 * tiles <= cus ? std::max(1, std::min({cus / tiles, 8, KT / 8})) : 1;
+    const int kps = piece_len(pieces);
+    pieces = (KT + kps - 1) / kps;
+    float *part = nullptr;
+    if (pieces > 1)
+      part = static_cast<float *>(swamp::stream_workspace(s, size_t(pieces) * mn * sizeof(float)));
+    if (pieces > 1 && !part)
+      zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
+    const Work wk{tiles_m, tiles_n, 0, 1, pieces, kps, part};
+    if (int rc = launch_tiles<DT, 2>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    if (pieces > 1 && part) {
+      split_reduce_kernel<<<unsigned((mn + 255) / 256), 256, 0, s>>>(part, y, pieces, mn);
+      if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+    }
+    return SWAMP_OK;
+  }
   if (2 * tiles <= cus) {
     auto est_us = [&](double step_us, int pieces) {
       double t_us = double(piece_len(pieces)) * step_us;

@@ -670,12 +670,12 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     }
     return SWAMP_OK;
   }
-  // Batches of more than 32 tokens written over y run as the prefill GEMM
-  // on x rounded to bf16 (in the stream's activation workspace): past two
-  // passes of 16 tokens its 256-token tiles cost less than streaming the
-  // weights again per pass (8B Q4_0 gate+up at 64 tokens: 64 us against
-  // 107 us).  Without the workspace the passes below run instead.
-  if (n_tok > 2 * kTok && !accumulate && n_cols % 64 == 0 &&
+  // Batches of more than 16 tokens written over y run as the prefill GEMM
+  // on x rounded to bf16 (in the stream's activation workspace): its
+  // 64-token tiles cost less than streaming the weights again per pass of
+  // 16 (8B Q4_0 gate+up at 24 tokens: 36 us against 50 us; at 64: 42 us
+  // against 107 us).  Without the workspace the passes below run instead.
+  if (n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
       size_t(n_tok) * size_t(n_cols) * 2 <= size_t(UINT32_MAX)) {
     const size_t n = size_t(n_tok) * size_t(n_cols);
     void *xb = swamp::stream_workspace(s, n * 2, 1);

@@ -170,8 +170,8 @@ def test_no_kernel_uses_scratch(asm):
 def test_gemm_wait_counts_match_emitted_loads(asm):
     lines = asm["gemm.hip"]
     kernels = list(_gemm_kernels(lines))
-    # three weight formats x (full tile, half tile)
-    assert len(kernels) == 6, [k for k, _ in kernels]
+    # three weight formats x (full, half, quarter tile)
+    assert len(kernels) == 9, [k for k, _ in kernels]
     bad = [(name, p) for name, body in kernels for p in [_gemm_wait_problems(body)] if p]
     assert not bad, bad
 

@@ -234,7 +234,7 @@ def test_gemv_multi(pkg, orc, torch_dev):
 @pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19, 33, 70])
 @pytest.mark.parametrize("rows,cols", [(1000, 4096), (256, 14336)])
 def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
-    # 1 token: the decode GEMV; 33 and 70: the prefill GEMM on bf16-rounded x
+    # 1 token: the decode GEMV; 19, 33 and 70: the prefill GEMM on bf16-rounded x
     torch = torch_dev
     raw = weights(pkg, dtype, rows, cols, mid=n_tok)
     xs = acts(pkg, n_tok, cols, mid=n_tok)
@@ -342,7 +342,7 @@ def test_batched_two_streams(pkg, torch_dev):
 def test_batched_accumulate(pkg, orc, torch_dev, cols, n_tok):
     """accumulate=1 is the kernel contract of fused_gemv_q4k_batched
     (out += W x, fused_gemv_q4k.rs:694); it keeps every pass, of one token
-    or of more than 32, on the small-batch kernel."""
+    or of more than 16, on the small-batch kernel."""
     torch = torch_dev
     rows = 512
     raw = weights(pkg, Q4_K, rows, cols, mid=3)
@@ -390,7 +390,7 @@ def test_gemm_bf16_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
 # tiles; at most half a round: full tiles in 2 and in 5 K pieces summed
 # through the workspace; short K (8 steps): half tiles.
 DECOMP_CASES = [(2048, 8192, 4096), (1900, 28572, 4096), (2048, 6144, 4096), (2048, 4096, 14336),
-                (512, 6144, 4096), (100, 600, 512)]
+                (512, 6144, 4096), (100, 600, 512), (48, 28672, 4096), (64, 4096, 14336), (1, 600, 1024)]
 
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])

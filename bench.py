@@ -169,7 +169,8 @@ SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 81
 
 def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
-    (lm_head Q8_0) for 1, 4, 8 and 16 tokens, the 70B Q4_K layer as
+    (lm_head Q8_0) for 1, 4, 8, 16 and 64 tokens (64: the entry point's
+    prefill-GEMM route), the 70B Q4_K layer as
     batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, and the 70B
     layer as a 4096-token bf16 prefill GEMM.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU
@@ -200,7 +201,7 @@ def run_sweep(pkg, torch, np, stream, lib):
             raise pkg.GpuError(rc, what)
 
     for label, shapes, sigma in (("llama3-8b", SWEEP_8B, 0.02), ("llama3-70b", SWEEP_70B, 0.015)):
-        for n_tok in ((1, 4, 8, 16) if label == "llama3-8b" else (1,)):
+        for n_tok in ((1, 4, 8, 16, 64) if label == "llama3-8b" else (1,)):
             per, tot_b, tot_us = [], 0, 0.0
             for i, (name, rows, k) in enumerate(shapes):
                 dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K

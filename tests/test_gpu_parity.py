@@ -304,7 +304,10 @@ def test_batched_two_streams(pkg, torch_dev):
     kept per (device, stream): calls queued on two streams at once give the
     same bits as the same calls run one after another on one stream."""
     torch = torch_dev
-    cases = [(Q4_K, 16, 4096, 14336), (Q4_0, 8, 6144, 4096), (Q8_0, 12, 4096, 4096)]
+    # the last two run the GEMM route: bf16 x in one per-stream buffer, K
+    # pieces in the other
+    cases = [(Q4_K, 16, 4096, 14336), (Q4_0, 8, 6144, 4096), (Q8_0, 12, 4096, 4096),
+             (Q4_0, 40, 4096, 4096), (Q4_K, 64, 6144, 4096)]
     bufs = []
     for i, (dt, n_tok, rows, cols) in enumerate(cases):
         raw = weights(pkg, dt, rows, cols, mid=120 + i)

@@ -26,6 +26,10 @@
 #ifndef SWAMP_GGUF_H
 #define SWAMP_GGUF_H
 
+#ifndef SWAMP_API
+#define SWAMP_API __attribute__((visibility("default")))
+#endif
+
 #include <stddef.h>
 #include <stdint.h>
 
@@ -54,48 +58,48 @@ typedef struct swamp_gguf swamp_gguf;
 
 /* GgufFile::open (mmap.rs:27-31) + parse.  On success *out is a handle to
  * close with swamp_gguf_close. */
-int swamp_gguf_open(const char *path, swamp_gguf **out);
-void swamp_gguf_close(swamp_gguf *g);
+SWAMP_API int swamp_gguf_open(const char *path, swamp_gguf **out);
+SWAMP_API void swamp_gguf_close(swamp_gguf *g);
 
 /* Header facts: version, tensor count (n_tensors, mmap.rs:119-121), the
  * data-section offset (data_offset) and the file size (file_size). */
-uint32_t swamp_gguf_version(const swamp_gguf *g);
-int64_t swamp_gguf_n_tensors(const swamp_gguf *g);
-int64_t swamp_gguf_n_kv(const swamp_gguf *g);
-uint64_t swamp_gguf_data_offset(const swamp_gguf *g);
-uint64_t swamp_gguf_file_size(const swamp_gguf *g);
+SWAMP_API uint32_t swamp_gguf_version(const swamp_gguf *g);
+SWAMP_API int64_t swamp_gguf_n_tensors(const swamp_gguf *g);
+SWAMP_API int64_t swamp_gguf_n_kv(const swamp_gguf *g);
+SWAMP_API uint64_t swamp_gguf_data_offset(const swamp_gguf *g);
+SWAMP_API uint64_t swamp_gguf_file_size(const swamp_gguf *g);
 
 /* Tensor i (file order): name (NUL-terminated), dtype, number of dims and
  * up to 4 dims (shape[0] = n_cols), the ABSOLUTE byte offset in the file
  * (the reference adds data_offset, mmap.rs:81-86) and nbytes.  Any output
  * pointer may be NULL.  i out of range -> SWAMP_EINVAL; more than 4 dims
  * fill the first 4. */
-int swamp_gguf_tensor_info(const swamp_gguf *g, int64_t i, const char **name, uint32_t *dtype,
+SWAMP_API int swamp_gguf_tensor_info(const swamp_gguf *g, int64_t i, const char **name, uint32_t *dtype,
                            int *n_dims, uint64_t dims[4], uint64_t *offset, uint64_t *nbytes);
 
 /* GgufFile::tensor (mmap.rs:96-99): index of the first tensor named
  * `name`, or SWAMP_ENOTFOUND (tensor_or_err, :101-105). */
-int64_t swamp_gguf_find(const swamp_gguf *g, const char *name);
+SWAMP_API int64_t swamp_gguf_find(const swamp_gguf *g, const char *name);
 
 /* GgufFile::tensor_raw_bytes (mmap.rs:110-117): host pointer into the
  * mapping and length; SWAMP_ETENSOR when the range passes the end. */
-int swamp_gguf_tensor_raw(const swamp_gguf *g, int64_t i, const void **ptr, size_t *len);
+SWAMP_API int swamp_gguf_tensor_raw(const swamp_gguf *g, int64_t i, const void **ptr, size_t *len);
 
 /* Copy tensor i's raw bytes into the device buffer d_dst (dst_len bytes
  * available) on `stream` (hipStream_t as void*, NULL = default).  The copy
  * is complete when the call returns (the source is pageable mapped memory).
  * dst_len < nbytes -> SWAMP_ESHAPE; copy failure -> SWAMP_ELAUNCH. */
-int swamp_gguf_upload(const swamp_gguf *g, int64_t i, void *d_dst, size_t dst_len, void *stream);
+SWAMP_API int swamp_gguf_upload(const swamp_gguf *g, int64_t i, void *d_dst, size_t dst_len, void *stream);
 
 /* Metadata lookup (Metadata::get_u32 / get_u64 / get_f32 / get_str,
  * metadata.rs:263-292).  Conversions follow MetadataValue::as_u32 /
  * as_u64 / as_f32 (metadata.rs:60-90); a key that is absent or does not
  * convert -> SWAMP_ENOTFOUND.  The string is not NUL-terminated: use len. */
-int swamp_gguf_meta_type(const swamp_gguf *g, const char *key, uint32_t *type);
-int swamp_gguf_meta_u32(const swamp_gguf *g, const char *key, uint32_t *out);
-int swamp_gguf_meta_u64(const swamp_gguf *g, const char *key, uint64_t *out);
-int swamp_gguf_meta_f32(const swamp_gguf *g, const char *key, float *out);
-int swamp_gguf_meta_str(const swamp_gguf *g, const char *key, const char **str, size_t *len);
+SWAMP_API int swamp_gguf_meta_type(const swamp_gguf *g, const char *key, uint32_t *type);
+SWAMP_API int swamp_gguf_meta_u32(const swamp_gguf *g, const char *key, uint32_t *out);
+SWAMP_API int swamp_gguf_meta_u64(const swamp_gguf *g, const char *key, uint64_t *out);
+SWAMP_API int swamp_gguf_meta_f32(const swamp_gguf *g, const char *key, float *out);
+SWAMP_API int swamp_gguf_meta_str(const swamp_gguf *g, const char *key, const char **str, size_t *len);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,10 @@
 #ifndef SWAMP_QMM_H
 #define SWAMP_QMM_H
 
+#ifndef SWAMP_API
+#define SWAMP_API __attribute__((visibility("default")))
+#endif
+
 #include <stddef.h>
 #include <stdint.h>
 
@@ -52,16 +56,16 @@ enum {
  * for the matmul library: selects the current device, creates its context
  * and caches its CU count.  Idempotent; optional (every entry point calls
  * it on first use). */
-int swamp_gpu_init(void);
+SWAMP_API int swamp_gpu_init(void);
 
 /* Text for a return code (static storage). */
-const char *swamp_strerror(int code);
+SWAMP_API const char *swamp_strerror(int code);
 
 /* GgmlDType::block_size / type_size / nbytes_for (swamp-gguf/src/dtype.rs:
  * 79-89, 92-132, 135-139).  0 for an unknown code. */
-size_t swamp_block_size(uint32_t dtype);
-size_t swamp_type_size(uint32_t dtype);
-size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
+SWAMP_API size_t swamp_block_size(uint32_t dtype);
+SWAMP_API size_t swamp_type_size(uint32_t dtype);
+SWAMP_API size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
 
 /* quant::dequantize (swamp-gguf/src/quant/mod.rs:18-33) on the device, for
  * F32, F16, BF16, Q4_0 (q4_0.rs:11-39), Q8_0 (q8_0.rs:15-40), Q4_K
@@ -69,7 +73,7 @@ size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
  * reference's scalar CPU dequantizer (NaN inputs give NaN outputs).
  * raw_len < nbytes_for(dtype, n) -> SWAMP_ESHAPE (the reference's
  * BufferTooSmall, q4_0.rs:15-20). */
-int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
+SWAMP_API int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
                    float *d_dst, size_t n, void *stream);
 
 /* Decode GEMV, y = W x, OVERWRITING y[0..n_rows).
@@ -85,7 +89,7 @@ int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
  * exponent field is 1..30; the reference's private f16 decode
  * (fused_gemv_q6k.rs:11-21) mis-decodes zero and subnormal d, and its SIMD
  * arms read the int8 scales as unsigned (:71-74, :164-167). */
-int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
+SWAMP_API int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
                 const float *d_x, float *d_y, int n_rows, int n_cols,
                 void *stream);
 
@@ -95,7 +99,7 @@ int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
  * (fused_gemv_q4k.rs:401-460).  All matrices share n_cols; dtypes may differ
  * per matrix.  At most SWAMP_MULTI_MAX matrices. */
 #define SWAMP_MULTI_MAX 8
-int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
+SWAMP_API int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
                       const void *const *d_ws, const size_t *w_lens,
                       const int *row_counts, const float *d_x,
                       float *const *d_ys, int n_cols, void *stream);
@@ -110,7 +114,7 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
  * squares is reduced in a different order than the reference's sequential
  * loop.  n_cols <= 32768 and a whole number of 64-weight items (multiple of
  * 64; 256 for Q4_K; 512 for Q6_K), else SWAMP_ESHAPE. */
-int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes,
+SWAMP_API int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes,
                         const void *const *d_ws, const size_t *w_lens,
                         const int *row_counts, const float *d_x,
                         const float *d_norm_w, float eps, float *const *d_ys,
@@ -123,7 +127,7 @@ int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes,
  * forward_linear + add_in_place (:216-220) at executor.rs:501-506.
  * d_gate, d_up: n_cols floats each, 16-byte aligned.  Shape rules as
  * swamp_qgemv_rmsnorm. */
-int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
+SWAMP_API int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
                        const float *d_gate, const float *d_up, float *d_y,
                        int n_rows, int n_cols, int accumulate, void *stream);
 
@@ -143,7 +147,7 @@ int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * GEMV per token written over y;
  * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
  * SWAMP_EDTYPE. */
-int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
+SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
                         const float *d_x, float *d_y, int n_tok, int n_rows,
                         int n_cols, int accumulate, void *stream);
 
@@ -163,7 +167,7 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  * GPU, K is split across workgroups whose partial tiles go to a scratch
  * buffer the library keeps per (device, stream), summed in piece order by
  * a second kernel (deterministic); calls on one stream share it. */
-int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
+SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);
 
@@ -180,10 +184,10 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
  * Inputs 16-byte aligned, d_out 16-byte (fp32) or 8-byte (bf16) aligned;
  * n_cols and n multiples of 4 (SWAMP_ESHAPE); out_type other than F32 /
  * BF16: SWAMP_EDTYPE. */
-int swamp_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps,
+SWAMP_API int swamp_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps,
                        void *d_out, uint32_t out_type, int n_tok, int n_cols,
                        void *stream);
-int swamp_swiglu(const float *d_gate, const float *d_up, void *d_out,
+SWAMP_API int swamp_swiglu(const float *d_gate, const float *d_up, void *d_out,
                  uint32_t out_type, size_t n, void *stream);
 
 /* Activations to Q8_0 blocks on the device (the int8 GEMM's input):
@@ -191,7 +195,7 @@ int swamp_swiglu(const float *d_gate, const float *d_up, void *d_out,
  * n / 32 * 34 bytes.  Per block d = amax / 127 rounded to f16,
  * q = round-half-away(x / d_unrounded) -- the block formula of the host
  * quantizer swamp_quantize (swamp_quant.h). */
-int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n,
+SWAMP_API int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n,
                         void *stream);
 
 /* ---- the reference's two existing C exports, host-pointer semantics ---- */
@@ -200,14 +204,14 @@ int swamp_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size_t n,
  * zeroes out and writes W x.  Null pointer or n_cols % 256 != 0 -> silent
  * return, like the reference.  Stages through device memory on the current
  * device and synchronizes before returning. */
-void swamp_fused_gemv_q4k(const uint8_t *w_raw, const float *x, float *out,
+SWAMP_API void swamp_fused_gemv_q4k(const uint8_t *w_raw, const float *x, float *out,
                           int n_rows, int n_cols);
 
 /* swamp_gemv_q8_vnni (swamp-kernels/src/lib.rs:452-482): HOST pointers,
  * exact int32 dot of two int8 vectors times scale; null or k <= 0 -> 0.0f.
  * Computed on the device (staged), synchronizes before returning; returns
  * NaN if the device step fails. */
-float swamp_gemv_q8_vnni(const int8_t *weights, const int8_t *activations,
+SWAMP_API float swamp_gemv_q8_vnni(const int8_t *weights, const int8_t *activations,
                          int k, float scale);
 
 #ifdef __cplusplus

@@ -29,6 +29,10 @@
 #ifndef SWAMP_QUANT_H
 #define SWAMP_QUANT_H
 
+#ifndef SWAMP_API
+#define SWAMP_API __attribute__((visibility("default")))
+#endif
+
 #include <stddef.h>
 #include <stdint.h>
 
@@ -38,26 +42,26 @@ extern "C" {
 
 /* IEEE conversions with round-to-nearest-even (what half::f16::from_f32 and
  * half::bf16::from_f32 do). */
-uint16_t swamp_f32_to_f16(float f);
-uint16_t swamp_f32_to_bf16(float f);
-void swamp_f32_to_bf16_array(const float *src, uint16_t *dst, size_t n);
+SWAMP_API uint16_t swamp_f32_to_f16(float f);
+SWAMP_API uint16_t swamp_f32_to_bf16(float f);
+SWAMP_API void swamp_f32_to_bf16_array(const float *src, uint16_t *dst, size_t n);
 
 /* rows x cols i.i.d. N(0, sigma^2) floats.  Row r draws from its own
  * splitmix64 stream seeded with seed ^ ((r + 1) * 0xD1B54A32D192ED03), and
  * Box-Muller in double precision turns pairs of draws into two normals. */
-int swamp_fill_normal(uint64_t seed, float sigma, float *dst, size_t rows,
+SWAMP_API int swamp_fill_normal(uint64_t seed, float sigma, float *dst, size_t rows,
                       size_t cols, int n_threads);
 
 /* Quantize rows x cols floats (row-major, cols a multiple of the block
  * size) into dtype blocks, row after row.  dtype: 2 = Q4_0, 8 = Q8_0,
  * 12 = Q4_K, 14 = Q6_K.  dst holds rows * cols / block * type_size bytes. */
-int swamp_quantize(uint32_t dtype, const float *src, uint8_t *dst, size_t rows,
+SWAMP_API int swamp_quantize(uint32_t dtype, const float *src, uint8_t *dst, size_t rows,
                    size_t cols, int n_threads);
 
 /* swamp_fill_normal followed by swamp_quantize, one row at a time, so a
  * 128256 x 8192 matrix never needs its f32 copy in memory.  Produces the
  * same bytes as the two-step call with the same seed. */
-int swamp_synth_quantized(uint32_t dtype, uint64_t seed, float sigma,
+SWAMP_API int swamp_synth_quantized(uint32_t dtype, uint64_t seed, float sigma,
                           uint8_t *dst, size_t rows, size_t cols,
                           int n_threads);
 

@@ -50,6 +50,15 @@ GGUF_SYMBOLS = (
     "swamp_gguf_meta_type", "swamp_gguf_meta_u32", "swamp_gguf_meta_u64", "swamp_gguf_meta_f32",
     "swamp_gguf_meta_str",
 )
+# Every symbol include/swamp_gpu.h declares: the device-management functions
+# the reference's bridge resolves by name (swamp-gpu/src/lib.rs:62-71,
+# :110-142, :239-347, :599-665).
+DEVICE_SYMBOLS = (
+    "gpu_init", "gpu_alloc", "gpu_free", "gpu_copy_to_device", "gpu_copy_to_host", "gpu_sync",
+    "gpu_stream_create", "gpu_stream_destroy", "gpu_stream_synchronize",
+    "gpu_copy_to_device_async", "gpu_copy_to_host_async", "gpu_event_create",
+    "gpu_event_record", "gpu_event_synchronize", "gpu_event_elapsed_ms", "gpu_event_destroy",
+)
 QUANT_SYMBOLS = (
     "swamp_f32_to_f16", "swamp_f32_to_bf16", "swamp_f32_to_bf16_array",
     "swamp_fill_normal", "swamp_quantize", "swamp_synth_quantized",
@@ -133,6 +142,23 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_gguf_meta_f32": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
         "swamp_gguf_meta_str": (i32, [c_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
                                       ctypes.POINTER(c_size)]),
+        # device management (include/swamp_gpu.h)
+        "gpu_init": (i32, []),
+        "gpu_alloc": (c_vp, [c_size]),
+        "gpu_free": (None, [c_vp]),
+        "gpu_copy_to_device": (i32, [c_vp, c_vp, c_size]),
+        "gpu_copy_to_host": (i32, [c_vp, c_vp, c_size]),
+        "gpu_sync": (i32, []),
+        "gpu_stream_create": (c_vp, []),
+        "gpu_stream_destroy": (None, [c_vp]),
+        "gpu_stream_synchronize": (i32, [c_vp]),
+        "gpu_copy_to_device_async": (i32, [c_vp, c_vp, c_size, c_vp]),
+        "gpu_copy_to_host_async": (i32, [c_vp, c_vp, c_size, c_vp]),
+        "gpu_event_create": (c_vp, []),
+        "gpu_event_record": (i32, [c_vp, c_vp]),
+        "gpu_event_synchronize": (i32, [c_vp]),
+        "gpu_event_elapsed_ms": (ctypes.c_float, [c_vp, c_vp]),
+        "gpu_event_destroy": (None, [c_vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

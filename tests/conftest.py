@@ -48,3 +48,21 @@ def fixtures():
     import json
     with open(os.path.join(REPO, "tests", "golden", "fixtures.json")) as f:
         return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def errlog():
+    """record(case, err): print the normalized error a parity case reached
+    and, when SWAMP_PARITY_LOG names a file, append it there as one JSON
+    line, so the precision of each path is visible from run to run."""
+    import json
+    path = os.environ.get("SWAMP_PARITY_LOG")
+
+    def record(case, err, **extra):
+        print(f"[parity] {case}: max normalized error {err:.3e}", flush=True)
+        if path:
+            with open(path, "a") as f:
+                f.write(json.dumps(dict(case=case, err=float(err), **extra)) + "\n")
+        return err
+
+    return record

@@ -12,10 +12,10 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared(header):
+def declared(header, prefix="swamp_"):
     text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(swamp_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"[a-z0-9_]+)\s*\(", text)))
 
 
 def exported(path):
@@ -38,6 +38,27 @@ def test_gpu_lib_exports_gguf_header(pkg):
     assert set(names) == set(pkg.GGUF_SYMBOLS)
     syms = exported(pkg.GPU_LIB_PATH)
     assert not [n for n in names if n not in syms]
+
+
+def test_gpu_lib_exports_device_header(pkg):
+    """The device-management functions the reference's bridge looks up by
+    name in libswamp_gpu.so (swamp-gpu/src/lib.rs)."""
+    names = declared("swamp_gpu.h", prefix="gpu_")
+    assert set(names) == set(pkg.DEVICE_SYMBOLS)
+    syms = exported(pkg.GPU_LIB_PATH)
+    assert not [n for n in names if n not in syms]
+    pkg.gpu_lib()
+
+
+def test_gpu_lib_exports_nothing_else(pkg):
+    """Only what the public headers declare is exported: the internal
+    launchers and helpers are hidden (the HIP runtime's per-unit ids
+    aside)."""
+    public = (set(declared("swamp_qmm.h")) | set(declared("swamp_gguf.h")) |
+              set(declared("swamp_gpu.h", prefix="gpu_")))
+    extra = [n for n in exported(pkg.GPU_LIB_PATH)
+             if n not in public and not n.startswith("__hip_cuid_")]
+    assert not extra, extra
 
 
 def test_quant_lib_exports_header(pkg):

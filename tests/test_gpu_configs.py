@@ -1,0 +1,208 @@
+"""GPU parity at the full shapes of the five benchmark configurations, through
+the C ABI, against the oracle on row and token subsets (the kernels run on
+the whole matrix; the oracle checks the first, a middle and the last rows,
+and tokens at tile edges).  Each case records the max normalized error it
+reached (errlog fixture).
+
+  config 1/2  Q4_0 decode GEMV at Llama-3-8B shapes
+  config 3    Q4_K small batch, N = 1, 4, 8, 16, with the Q8_0 lm_head
+              (benchmark_q4k_batched.rs:70-108 call pattern)
+  config 4    Q4_0 prefill GEMM at M = 512 and 2048, bf16 x and Q8_0 x
+              (executor.rs:106-110 call pattern)
+  config 5    Llama-3-70B Q4_K: decode GEMV and the 4096-token bf16 prefill
+              GEMM, with the Q8_0 lm_head
+
+The contract bound is TOL = 1e-3 (max_r |y - y_ref| / (||W_r|| ||x||)); each
+path also has a tighter bound of its own arithmetic, below."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, F32, BF16 = 2, 8, 12, 0, 30
+TOL = 1e-3
+# Per-path bounds, each a few times the error the path's rounding of its
+# operands gives on these N(0, 1) activations and N(0, sigma) weights:
+#   GEMV, fp32 x and fp32 sums (the reference's arithmetic): summation order only;
+#   small batch (2..16 tokens), x rounded to fp16 (2^-11 relative);
+#   GEMM, x and the dequantized weights rounded to bf16 (2^-8 relative each);
+#   int8 GEMM, x quantized to Q8_0 (the oracle multiplies the same Q8_0 x).
+BOUND = {"gemv": 1e-3, "batched_f16": 1e-4, "gemm_bf16": 4e-4, "gemm_i8": 1e-5}
+
+LLAMA8B = {"qkv": (6144, 4096), "o_proj": (4096, 4096), "gate_up": (28672, 4096),
+           "down": (4096, 14336), "lm_head": (128256, 4096)}
+LLAMA70B = {"qkv": (10240, 8192), "o_proj": (8192, 8192), "gate_up": (57344, 8192),
+            "down": (8192, 28672), "lm_head": (128256, 8192)}
+
+
+@pytest.fixture(scope="module")
+def torch_dev(pkg):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    pkg.init()
+    return torch
+
+
+class Weights:
+    """Host bytes and one device copy per (dtype, shape, sigma), generated
+    once per module (the 70B Q8_0 lm_head is 1.1 GB)."""
+
+    def __init__(self, pkg, torch):
+        self.pkg, self.torch, self.cache = pkg, torch, {}
+
+    def get(self, dtype, rows, cols, sigma):
+        key = (dtype, rows, cols, sigma)
+        if key not in self.cache:
+            if len(self.cache) >= 3:  # keep device memory bounded
+                self.cache.pop(next(iter(self.cache)))
+            seed = 0x5EED ^ (dtype << 40) ^ (rows << 20) ^ cols
+            raw = self.pkg.synth_quantized(dtype, seed, sigma, rows, cols)
+            self.cache[key] = (raw, self.torch.from_numpy(raw).cuda())
+        return self.cache[key]
+
+
+@pytest.fixture(scope="module")
+def W(pkg, torch_dev):
+    w = Weights(pkg, torch_dev)
+    yield w
+    w.cache.clear()
+    torch_dev.cuda.empty_cache()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def row_sets(rows):
+    return [(0, min(rows, 1024)), (rows // 2 - 256, rows // 2 + 256), (max(0, rows - 1024), rows)]
+
+
+def check_rows(pkg, orc, dtype, raw, cols, y, xs, rows):
+    """max normalized error of y [T, rows] against the oracle's
+    forward_linear_batch on xs [T, cols], over row_sets(rows)."""
+    rb = pkg.row_bytes(dtype, cols)
+    worst = 0.0
+    for r0, r1 in row_sets(rows):
+        sub = raw[r0 * rb:r1 * rb]
+        ref = orc.forward_linear_batch(dtype, sub, xs, r1 - r0, cols, 8)
+        deq = orc.dequantize(dtype, sub, (r1 - r0) * cols).reshape(r1 - r0, cols)
+        worst = max(worst, orc.normalized_error(y[:, r0:r1], ref, deq, xs))
+    return worst
+
+
+# ------------------------------------------------------------ decode GEMV
+
+GEMV_CASES = ([("8b", n, Q4_0, 0.02) + LLAMA8B[n] for n in LLAMA8B] +
+              [("70b", n, Q8_0 if n == "lm_head" else Q4_K, 0.015) + LLAMA70B[n]
+               for n in LLAMA70B])
+
+
+@pytest.mark.parametrize("model,name,dtype,sigma,rows,cols", GEMV_CASES,
+                         ids=[f"{c[0]}-{c[1]}" for c in GEMV_CASES])
+def test_config_decode_gemv(pkg, orc, torch_dev, W, errlog, model, name, dtype, sigma, rows, cols):
+    """Configs 1/2 (8B Q4_0) and 5 (70B Q4_K, Q8_0 lm_head): swamp_qgemv at
+    batch 1 on the full matrix."""
+    torch = torch_dev
+    raw, d_w = W.get(dtype, rows, cols, sigma)
+    x = pkg.fill_normal(0xA11CE ^ rows ^ cols, 1.0, 1, cols)
+    print(f"[gpu case] config decode gemv {model} {name} {rows}x{cols} dtype {dtype}", flush=True)
+    d_x = torch.from_numpy(x[0]).cuda()
+    d_y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), rows, cols,
+              stream(torch))
+    torch.cuda.synchronize()
+    y = d_y.cpu().numpy()[None, :]
+    assert np.isfinite(y).all()
+    err = errlog(f"gemv {model} {name}", check_rows(pkg, orc, dtype, raw, cols, y, x, rows),
+                 path="gemv")
+    assert err <= min(TOL, BOUND["gemv"])
+
+
+# ------------------------------------------------------------ small batch
+
+BATCH_CASES = [(n, Q8_0 if n == "lm_head" else Q4_K) + LLAMA8B[n] for n in LLAMA8B]
+
+
+@pytest.mark.parametrize("n_tok", [1, 4, 8, 16])
+@pytest.mark.parametrize("name,dtype,rows,cols", BATCH_CASES, ids=[c[0] for c in BATCH_CASES])
+def test_config3_small_batch(pkg, orc, torch_dev, W, errlog, name, dtype, rows, cols, n_tok):
+    """Config 3: swamp_qgemv_batched (accumulate = 0, forward_linear_batch)
+    at the five 8B shapes, Q4_K with the Q8_0 lm_head; every work
+    decomposition the sweep times (K groups for the small matrices, the
+    Wk = 2 phase form for gate+up, Wk = 1 for the lm_head)."""
+    torch = torch_dev
+    raw, d_w = W.get(dtype, rows, cols, 0.02)
+    xs = pkg.fill_normal(0xA11CE ^ (n_tok << 8) ^ rows, 1.0, n_tok, cols)
+    print(f"[gpu case] config3 small batch {name} {rows}x{cols} n_tok {n_tok}", flush=True)
+    d_x = torch.from_numpy(xs).cuda()
+    d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv_batched(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                      rows, cols, False, stream(torch))
+    torch.cuda.synchronize()
+    y = d_y.cpu().numpy()
+    assert np.isfinite(y).all()
+    path = "gemv" if n_tok == 1 else "batched_f16"
+    err = errlog(f"small batch {name} n_tok={n_tok}",
+                 check_rows(pkg, orc, dtype, raw, cols, y, xs, rows), path=path)
+    assert err <= min(TOL, BOUND[path])
+
+
+# ------------------------------------------------------------ prefill GEMM
+
+def _gemm(pkg, orc, torch, W, dtype, sigma, rows, cols, m, x_type, mid):
+    raw, d_w = W.get(dtype, rows, cols, sigma)
+    x = pkg.fill_normal(0xA11CE ^ mid ^ m, 1.0, m, cols)
+    if x_type == BF16:
+        xb = pkg.to_bf16_bits(x)
+        x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
+        d_x = torch.from_numpy(xb.view(np.int16)).cuda()
+    else:
+        d_f = torch.from_numpy(x).cuda()
+        d_x = torch.empty(m * cols // 32 * 34, dtype=torch.uint8, device="cuda")
+        pkg.quantize_q8_0(d_f.data_ptr(), F32, d_x.data_ptr(), m * cols, stream(torch))
+        xq = pkg.quantize(Q8_0, x)
+        x_fed = None
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), x_type, d_y.data_ptr(), m, rows,
+              cols, stream(torch))
+    torch.cuda.synchronize()
+    if x_type == Q8_0:
+        assert np.array_equal(d_x.cpu().numpy(), xq)  # device quantizer = host quantizer
+        x_fed = orc.dequantize(Q8_0, xq, m * cols).reshape(m, cols)
+    toks = sorted(set(t for t in [0, 1, 127, 128, 255, 256, m // 2, m - 257, m - 256, m - 1]
+                      if 0 <= t < m))
+    y = d_y[toks].cpu().numpy()
+    del d_y
+    assert np.isfinite(y).all()
+    return check_rows(pkg, orc, dtype, raw, cols, y, x_fed[toks], rows)
+
+
+PREFILL8B = ["gate_up", "down", "qkv"]
+
+
+@pytest.mark.parametrize("x_type", [BF16, Q8_0], ids=["bf16", "q8_0"])
+@pytest.mark.parametrize("m", [512, 2048])
+@pytest.mark.parametrize("name", PREFILL8B)
+def test_config4_prefill(pkg, orc, torch_dev, W, errlog, name, m, x_type):
+    """Config 4: Q4_0 prefill GEMM at the 8B FFN and attention shapes, bf16
+    x on the bf16 matrix cores and Q8_0 x on the int8 matrix cores."""
+    rows, cols = LLAMA8B[name]
+    print(f"[gpu case] config4 prefill {name} m {m} x_type {x_type}", flush=True)
+    err = _gemm(pkg, orc, torch_dev, W, Q4_0, 0.02, rows, cols, m, x_type, mid=rows)
+    path = "gemm_bf16" if x_type == BF16 else "gemm_i8"
+    errlog(f"prefill 8b {name} m={m} {'bf16' if x_type == BF16 else 'q8_0'}", err, path=path)
+    assert err <= min(TOL, BOUND[path])
+
+
+@pytest.mark.parametrize("name", list(LLAMA70B))
+def test_config5_prefill(pkg, orc, torch_dev, W, errlog, name):
+    """Config 5: the 4096-token bf16 prefill GEMM at the 70B shapes (Q4_K,
+    Q8_0 lm_head)."""
+    rows, cols = LLAMA70B[name]
+    dtype = Q8_0 if name == "lm_head" else Q4_K
+    print(f"[gpu case] config5 prefill {name} m 4096", flush=True)
+    err = _gemm(pkg, orc, torch_dev, W, dtype, 0.015, rows, cols, 4096, BF16, mid=rows)
+    errlog(f"prefill 70b {name} m=4096 bf16", err, path="gemm_bf16")
+    assert err <= min(TOL, BOUND["gemm_bf16"])

@@ -406,11 +406,10 @@ def main():
               f"{src.numel()}-byte device copy", flush=True)
         return
 
-    def launch(c, i):
+    def launch(c, i, fn=lib.swamp_qgemv):
         _, rows, k = DECODE_SHAPES[i]
         w = sets[c][i]
-        rc = lib.swamp_qgemv(pkg.Q4_0, w.data_ptr(), w.numel(), xs[i].data_ptr(),
-                             ys[i].data_ptr(), rows, k, s)
+        rc = fn(pkg.Q4_0, w.data_ptr(), w.numel(), xs[i].data_ptr(), ys[i].data_ptr(), rows, k, s)
         if rc != 0:
             raise pkg.GpuError(rc, "swamp_qgemv")
 
@@ -459,21 +458,45 @@ def main():
     # ---- per-matrix kernel times (outside the timed region) --------------
     # Each matrix alone, 20 back-to-back launches over the rotated copies,
     # queued behind a GPU sleep so the host never starves the GPU.
-    shapes = []
-    for i, (name, rows, k) in enumerate(DECODE_SHAPES):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        torch.cuda._sleep(20_000_000)
-        e0.record(stream)
-        for it in range(20):
-            launch(it % args.copies, i)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / 20
-        b = alg_bytes_gemv(18, rows, k)
-        shapes.append({"name": name, "rows": rows, "k": k, "bytes": b, "us": round(us, 2),
-                       "GB/s": round(b / (us * 1e-6) / 1e9, 1),
-                       "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    def per_matrix(fn):
+        out = []
+        for i, (name, rows, k) in enumerate(DECODE_SHAPES):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(20_000_000)
+            e0.record(stream)
+            for it in range(20):
+                launch(it % args.copies, i, fn)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / 20
+            b = alg_bytes_gemv(18, rows, k)
+            out.append({"name": name, "rows": rows, "k": k, "bytes": b, "us": round(us, 2),
+                        "GB/s": round(b / (us * 1e-6) / 1e9, 1),
+                        "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        return out
+
+    shapes = per_matrix(lib.swamp_qgemv)
+
+    # ---- the same step on swamp_qgemv_f16x (x rounded to fp16 inside the
+    # kernel): a separately labelled line, not the headline
+    for it in range(args.warmup):
+        for i in range(n):
+            launch(it % args.copies, i, lib.swamp_qgemv_f16x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for it in range(args.steps):
+        for i in range(n):
+            launch(it % args.copies, i, lib.swamp_qgemv_f16x)
+    torch.cuda.synchronize()
+    ms16 = (time.perf_counter() - t0) * 1e3 / args.steps
+    f16x = {"entry": "swamp_qgemv_f16x", "dtype": "q4_0 x f16 -> f32",
+            "note": "x rounded to fp16 per 64-weight run inside the kernel; not the reference's "
+                    "arithmetic",
+            "value": round(step_bytes / (ms16 * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "ms_per_step": round(ms16, 4),
+            "frac_hbm_peak": round(step_bytes / (ms16 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "shapes": per_matrix(lib.swamp_qgemv_f16x)}
 
     # ---- prefill GEMM, 2048 and 512 tokens, bf16 / Q8_0 activations ----------
     prefill = None
@@ -540,7 +563,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x f16 -> f32",
+        "dtype": "q4_0 x f32 -> f32",
         "data": "synthetic (W ~ N(0,0.02) quantized to Q4_0 on the host, x ~ N(0,1) fp32)",
         "config": {"workload": "llama3-8b decode layer sweep, Q4_0, batch 1: qkv 6144x4096, "
                                "o_proj 4096x4096, gate_up 28672x4096, down 4096x14336, "
@@ -550,6 +573,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "shapes": shapes,
+        "decode_f16x": f16x,
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)

@@ -80,6 +80,9 @@ SWAMP_API int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
  * Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the
  * kernels it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:
  * 59-82) and fused_gemv_q6k (fused_gemv_q6k.rs:22-41).
+ * Arithmetic as the reference's: the exact weight values times unrounded
+ * fp32 x, summed in fp32 (one rounding per multiply-add); only the order
+ * of the sums differs.
  * dtype Q4_0, Q8_0, Q4_K or Q6_K; n_cols a multiple of the block size (32,
  * or 256 for Q4_K and Q6_K); w_len >= nbytes_for(dtype, n_rows * n_cols);
  * d_w 4-byte aligned (16 for Q4_K), d_x 16-byte aligned.  n_cols == 0
@@ -92,6 +95,18 @@ SWAMP_API int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
 SWAMP_API int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len,
                 const float *d_x, float *d_y, int n_rows, int n_cols,
                 void *stream);
+
+/* The decode GEMV at reduced x precision, for callers that accept it:
+ * arguments, shapes and y as swamp_qgemv, but each 64-weight run of x is
+ * scaled by a power of two (exact) and rounded to fp16 (2^-11 relative)
+ * inside the kernel, and weight pairs meet x pairs in fp16 dot products
+ * with fp32 accumulation.  That halves the kernel's arithmetic per weight
+ * against swamp_qgemv's fp32 x; the results differ from the reference's
+ * fp32 arithmetic by about 1e-5 of ||W_r|| ||x|| (swamp_qgemv: about
+ * 1e-7).  No counterpart in the reference. */
+SWAMP_API int swamp_qgemv_f16x(uint32_t dtype, const void *d_w, size_t w_len,
+                               const float *d_x, float *d_y, int n_rows, int n_cols,
+                               void *stream);
 
 /* Several matrices that share one x (the engine's fused QKV and gate+up):
  * y_m = W_m x for m < n_mats, each OVERWRITTEN, one launch.

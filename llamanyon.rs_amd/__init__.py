@@ -37,7 +37,7 @@ MULTI_MAX = 8
 # Every symbol include/swamp_qmm.h declares.
 GPU_SYMBOLS = (
     "swamp_gpu_init", "swamp_strerror", "swamp_block_size", "swamp_type_size",
-    "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_multi",
+    "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_f16x", "swamp_qgemv_multi",
     "swamp_qgemv_rmsnorm", "swamp_qgemv_swiglu",
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
     "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
@@ -105,6 +105,7 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_nbytes_for": (c_size, [u32, c_size]),
         "swamp_qdequant": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp]),
         "swamp_qgemv": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
+        "swamp_qgemv_f16x": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
         "swamp_qgemv_multi": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
                                     ctypes.POINTER(c_size), ctypes.POINTER(i32), c_vp,
                                     ctypes.POINTER(c_vp), i32, c_vp]),
@@ -222,6 +223,13 @@ def qdequant(dtype: int, d_raw: int, raw_len: int, d_dst: int, n: int, stream: i
 def qgemv(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_rows: int, n_cols: int,
           stream: int = 0) -> None:
     _check(gpu_lib().swamp_qgemv(dtype, d_w, w_len, d_x, d_y, n_rows, n_cols, stream), "swamp_qgemv")
+
+
+def qgemv_f16x(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_rows: int, n_cols: int,
+               stream: int = 0) -> None:
+    """swamp_qgemv with x rounded to fp16 inside the kernel (faster, ~1e-5)."""
+    _check(gpu_lib().swamp_qgemv_f16x(dtype, d_w, w_len, d_x, d_y, n_rows, n_cols, stream),
+           "swamp_qgemv_f16x")
 
 
 def qgemv_multi(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int],

@@ -237,6 +237,18 @@ int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x,
   return swamp_launch_gemv(dtype, d_w, d_x, d_y, n_rows, n_cols, static_cast<hipStream_t>(stream));
 }
 
+int swamp_qgemv_f16x(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x, float *d_y,
+                     int n_rows, int n_cols, void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (!d_x || !d_y) return SWAMP_EINVAL;
+  if (!aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (n_rows == 0) return SWAMP_OK;
+  if (int rc = ensure_device(nullptr)) return rc;
+  if (n_cols == 0) return fill_zero(d_y, size_t(n_rows), static_cast<hipStream_t>(stream));
+  return swamp_launch_gemv_f16x(dtype, d_w, d_x, d_y, n_rows, n_cols,
+                                static_cast<hipStream_t>(stream));
+}
+
 int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
                       const size_t *w_lens, const int *row_counts, const float *d_x,
                       float *const *d_ys, int n_cols, void *stream) {

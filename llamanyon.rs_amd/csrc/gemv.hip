@@ -160,36 +160,56 @@ __global__ void __launch_bounds__(256) gemv_generic_q4k_kernel(const uint8_t *__
 
 }  // namespace
 
-int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
-                      int n_rows, int n_cols, hipStream_t s) {
+namespace {
+
+// Shapes the item kernel does not take: one wavefront per row (fp32 x).
+int launch_generic(uint32_t dtype, const void *d_w, const float *d_x, float *d_y, int n_rows,
+                   int n_cols, hipStream_t s) {
+  const int cus = swamp::device_info().num_cus;
+  const int blocks = std::min((n_rows + 3) / 4, cus * 8);
+  if (dtype == SWAMP_Q4_K)
+    gemv_generic_q4k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
+                                                   n_rows, n_cols);
+  else if (dtype == SWAMP_Q6_K)
+    gemv_generic_q6k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
+                                                   n_rows, n_cols);
+  else if (dtype == SWAMP_Q4_0)
+    gemv_generic_kernel<SWAMP_Q4_0><<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x,
+                                                           d_y, n_rows, n_cols);
+  else
+    gemv_generic_kernel<SWAMP_Q8_0><<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x,
+                                                           d_y, n_rows, n_cols);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
+
+template <bool kX32>
+int launch_one(uint32_t dtype, const void *d_w, const float *d_x, float *d_y, int n_rows,
+               int n_cols, hipStream_t s) {
   if (n_rows == 0) return SWAMP_OK;
-  if (!item_path_ok(dtype, n_cols)) {
-    const int cus = swamp::device_info().num_cus;
-    const int blocks = std::min((n_rows + 3) / 4, cus * 8);
-    if (dtype == SWAMP_Q4_K)
-      gemv_generic_q4k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
-                                                     n_rows, n_cols);
-    else if (dtype == SWAMP_Q6_K)
-      gemv_generic_q6k_kernel<<<blocks, 256, 0, s>>>(static_cast<const uint8_t *>(d_w), d_x, d_y,
-                                                     n_rows, n_cols);
-    else if (dtype == SWAMP_Q4_0)
-      gemv_generic_kernel<SWAMP_Q4_0><<<blocks, 256, 0, s>>>(
-          static_cast<const uint8_t *>(d_w), d_x, d_y, n_rows, n_cols);
-    else
-      gemv_generic_kernel<SWAMP_Q8_0><<<blocks, 256, 0, s>>>(
-          static_cast<const uint8_t *>(d_w), d_x, d_y, n_rows, n_cols);
-    return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
-  }
+  if (!item_path_ok(dtype, n_cols)) return launch_generic(dtype, d_w, d_x, d_y, n_rows, n_cols, s);
   MatSet ms;
   const void *ws[1] = {d_w};
   float *ys[1] = {d_y};
-  const int tr = tile_rows_for(dtype, n_cols, n_rows);
+  const int tr = tile_rows_for(dtype, n_cols, n_rows, kX32);
   build_matset(ms, 1, ws, ys, &n_rows, tr);
-  return dispatch<kProNone>(dtype, ms, d_x, Pro{}, n_cols, tr, s);
+  return dispatch<kProNone, kX32>(dtype, ms, d_x, Pro{}, n_cols, tr, s);
+}
+
+}  // namespace
+
+int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
+                      int n_rows, int n_cols, hipStream_t s) {
+  return launch_one<true>(dtype, d_w, d_x, d_y, n_rows, n_cols, s);
+}
+
+int swamp_launch_gemv_f16x(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
+                           int n_rows, int n_cols, hipStream_t s) {
+  return launch_one<false>(dtype, d_w, d_x, d_y, n_rows, n_cols, s);
 }
 
 int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
                             const int *row_counts, const float *d_x, float *const *d_ys,
                             int n_cols, hipStream_t s) {
-  return launch_multi<kProNone>(n_mats, dtypes, d_ws, row_counts, d_x, Pro{}, d_ys, n_cols, s);
+  return launch_multi<kProNone, true>(n_mats, dtypes, d_ws, row_counts, d_x, Pro{}, d_ys, n_cols,
+                                      s);
 }

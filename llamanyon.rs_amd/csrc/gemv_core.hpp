@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace {
 
@@ -322,6 +323,175 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf,
   }
 }
 
+// ---- fp32 x: the reference's arithmetic ------------------------------------
+// The default GEMV multiplies the exact weight codes by unrounded fp32 x and
+// sums in fp32, as forward_linear (linear.rs:81-85) and the scalar Q4_K
+// GEMV (fused_gemv_q4k.rs:484-504) do.  A weight pair still becomes an fp16
+// pair with one and-or (1024 + q, or 1024 + 16 q for a nibble left in
+// place); one packed fp16 add or fma then removes the magic offset, which
+// is exact (the results are small integers), leaving the signed code
+// (q - 8 for Q4_0, q for Q4_K, q - 32 for Q6_K).  V_FMA_MIX_F32 converts
+// each half to fp32 (exact) and fuses it with the fp32 x value and the fp32
+// partial sum: one rounding per weight, as in an fp32 FMA.  Q8_0 bytes are
+// converted with a sign-extending sub-dword convert.  The block scales are
+// applied per block (Q4_0, Q8_0, Q6_K: d * sum; Q4_K: (d sc) sum(q x) -
+// (dmin m) sum(x), with sum(x) per sub-block taken once per lane).
+// Per 8 nibbles: 1 shift + 4 and-or + 4 packed fp16 ops + 8 fma_mix.
+
+template <int DT>
+struct XFrag32 {
+  float x[64];   // the item's x in the order item_dot forms its weight pairs
+  float sa, sb;  // Q4_K: sum of x over sub-block A (items 0..31) and B (32..63)
+};
+
+__device__ __forceinline__ half2_t h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ half2_t h2c(float c) { return half2_t{(_Float16)c, (_Float16)c}; }
+
+// a += e.lo * x0, b += e.hi * x1 (two V_FMA_MIX_F32 with op_sel)
+__device__ __forceinline__ void fma2(half2_t e, float x0, float x1, float &a, float &b) {
+  a = __builtin_fmaf(float(e[0]), x0, a);
+  b = __builtin_fmaf(float(e[1]), x1, b);
+}
+
+template <int DT>
+__device__ __forceinline__ void build_xfrag(XFrag32<DT> &xf, const float4 (&x4)[16], bool valid) {
+  float xv[64];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    xv[4 * i] = x4[i].x; xv[4 * i + 1] = x4[i].y; xv[4 * i + 2] = x4[i].z; xv[4 * i + 3] = x4[i].w;
+  }
+#pragma unroll
+  for (int i = 0; i < 64; i++) xv[i] = valid ? xv[i] : 0.f;
+  if constexpr (DT == SWAMP_Q6_K) {
+    // pair 8t + 2j + e (group j, dword t, bytes e and e + 2) -> x[16t + 4j + 2e + h]
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) xf.x[16 * t + 4 * j + 2 * e + h] = xv[16 * j + 4 * t + e + 2 * h];
+  } else if constexpr (DT == SWAMP_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < 64; i++) xf.x[i] = xv[i];  // byte b of dword t is element 4t + b
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) xf.x[8 * t + 2 * p + h] = xv[nib_elem<DT>(t, p, h)];
+    if constexpr (DT == SWAMP_Q4_K) {
+      float sa = 0.f, sb = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        sa += xv[i];
+        sb += xv[32 + i];
+      }
+      xf.sa = sa;
+      xf.sb = sb;
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag32<DT> &xf, int item,
+                                          uint32_t m) {
+  if constexpr (DT == SWAMP_Q4_0) {
+    const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
+    const float d1 = swamp::f16_bits_to_f32(r.d[4] >> 16);
+    const half2_t lo_off = h2c(1032.f), hi_mul = h2c(0.0625f), hi_off = h2c(72.f);
+    float s0a = 0.f, s0b = 0.f, s1a = 0.f, s1b = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const uint32_t w = t < 4 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1];
+      uint32_t P[4];
+      nib_pairs(w, m, P);
+      // (1024 + q) - 1032 = q - 8;  (1024 + 16 q) / 16 - 72 = q - 8
+      const half2_t E[4] = {h2(P[0]) - lo_off, h2(P[1]) - lo_off, h2(P[2]) * hi_mul - hi_off,
+                            h2(P[3]) * hi_mul - hi_off};
+      const float *x = xf.x + 8 * t;
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        if (t < 4) fma2(E[p], x[2 * p], x[2 * p + 1], s0a, s0b);
+        else fma2(E[p], x[2 * p], x[2 * p + 1], s1a, s1b);
+      }
+    }
+    return d0 * (s0a + s0b) + d1 * (s1a + s1b);
+  } else if constexpr (DT == SWAMP_Q8_0) {
+    const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
+    const float d1 = swamp::f16_bits_to_f32(r.d[8] >> 16);
+    float s0a = 0.f, s0b = 0.f, s1a = 0.f, s1b = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      const uint32_t w = t < 8 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1];
+      const float *x = xf.x + 4 * t;
+      float &a = t < 8 ? s0a : s1a;
+      float &b = t < 8 ? s0b : s1b;
+      a = __builtin_fmaf(float(int8_t(w)), x[0], a);
+      b = __builtin_fmaf(float(int8_t(w >> 8)), x[1], b);
+      a = __builtin_fmaf(float(int8_t(w >> 16)), x[2], a);
+      b = __builtin_fmaf(float(int32_t(w) >> 24), x[3], b);
+    }
+    return d0 * (s0a + s0b) + d1 * (s1a + s1b);
+  } else if constexpr (DT == SWAMP_Q6_K) {
+    const uint32_t sh = uint32_t(item & 4) >> 1;
+    const uint32_t ii = uint32_t(item & 1);
+    const uint32_t s01 = __builtin_amdgcn_alignbyte(r.s[1], r.s[0], sh);
+    const uint32_t s23 = __builtin_amdgcn_alignbyte(r.s[2], r.s[1], sh);
+    const float d = swamp::f16_bits_to_f32(__builtin_amdgcn_alignbyte(0u, r.d, sh) & 0xFFFFu);
+    const float sc0 = float(int(s01 << (24 - 8 * ii)) >> 24);
+    const float sc1 = float(int(s01 << (8 - 8 * ii)) >> 24);
+    const float sc2 = float(int(s23 << (24 - 8 * ii)) >> 24);
+    const float sc3 = float(int(s23 << (8 - 8 * ii)) >> 24);
+    const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, b45 = 0x00300030u, b89 = 0x03000300u;
+    // (1024 + q) - 1056 = q - 32;  (1024 + 16 q) / 16 - 96 = q - 32
+    const half2_t lo_off = h2c(1056.f), hi_mul = h2c(0.0625f), hi_off = h2c(96.f);
+    float g[4][2] = {};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t A = __builtin_amdgcn_alignbyte(r.a[t + 1], r.a[t], sh);
+      const uint32_t B = __builtin_amdgcn_alignbyte(r.b[t + 1], r.b[t], sh);
+      const uint32_t H = __builtin_amdgcn_alignbyte(r.h[t + 1], r.h[t], sh);
+      const uint32_t hA = H << 4, hB = H >> 4, hC = H << 2, hD = H >> 6;
+      const uint32_t sA = A >> 8, sB = B >> 8;
+      const half2_t E[8] = {
+          h2((A & lo) | (hA & b45) | m) - lo_off,           h2((sA & lo) | (hB & b45) | m) - lo_off,
+          h2((B & lo) | (hC & b45) | m) - lo_off,           h2((sB & lo) | (hD & b45) | m) - lo_off,
+          h2((A & hi) | (hA & b89) | m) * hi_mul - hi_off,  h2((sA & hi) | (hB & b89) | m) * hi_mul - hi_off,
+          h2((B & hi) | (hC & b89) | m) * hi_mul - hi_off,  h2((sB & hi) | (hD & b89) | m) * hi_mul - hi_off};
+      const float *x = xf.x + 16 * t;
+#pragma unroll
+      for (int k = 0; k < 8; k++) fma2(E[k], x[2 * k], x[2 * k + 1], g[k >> 1][0], g[k >> 1][1]);
+    }
+    return d * (sc0 * (g[0][0] + g[0][1]) + sc1 * (g[1][0] + g[1][1]) +
+                sc2 * (g[2][0] + g[2][1]) + sc3 * (g[3][0] + g[3][1]));
+  } else {
+    const float d = swamp::f16_bits_to_f32(r.h[0] & 0xFFFFu);
+    const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
+    uint32_t sc0, m0, sc1, m1;
+    q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
+    // (1024 + q) - 1024 = q;  (1024 + 16 q) / 16 - 64 = q
+    const half2_t lo_off = h2c(1024.f), hi_mul = h2c(0.0625f), hi_off = h2c(64.f);
+    float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      uint32_t P[4];
+      nib_pairs(r.q[t], m, P);
+      const float *x = xf.x + 8 * t;
+      fma2(h2(P[0]) - lo_off, x[0], x[1], sa0, sa1);
+      fma2(h2(P[1]) - lo_off, x[2], x[3], sa0, sa1);
+      fma2(h2(P[2]) * hi_mul - hi_off, x[4], x[5], sb0, sb1);
+      fma2(h2(P[3]) * hi_mul - hi_off, x[6], x[7], sb0, sb1);
+    }
+    // sum ((d sc) q - dmin m) x = (d sc) sum(q x) - (dmin m) sum(x), per sub-block
+    const float sv0 = d * float(sc0), mv0 = dmin * float(m0);
+    const float sv1 = d * float(sc1), mv1 = dmin * float(m1);
+    return (sv0 * (sa0 + sa1) - mv0 * xf.sa) + (sv1 * (sb0 + sb1) - mv1 * xf.sb);
+  }
+}
+
 // ---- wavefront reduction of kRows partial sums ---------------------------
 
 template <int kCtrl>
@@ -427,9 +597,9 @@ __device__ __forceinline__ int store_row(const TileRef &t, int tid) {
   return min(t.row0 + rr, t.nrows - 1);
 }
 
-template <int DT, int kPPT, int kRows, int kWaves, bool kAcc>
+template <int DT, int kPPT, int kRows, int kWaves, bool kAcc, class XF>
 __device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
-                                             const XFrag<DT> (&xf)[kPPT], const TileRef &t,
+                                             const XF (&xf)[kPPT], const TileRef &t,
                                              const int (&item)[kPPT],
                                              float (*red)[kRows], int tid, uint32_t m,
                                              float out_scale, float y_old) {
@@ -525,10 +695,13 @@ using swamp::silu_mul;
 // walks tiles blockIdx.x, + gridDim.x, ... of kRows rows each.  Since every
 // workgroup holds all of x, a prologue that needs the whole vector (the
 // RMSNorm sum of squares) is computed by each workgroup for itself.
-template <int DT, int kPPT, int kRows, int kWaves, bool kMulti, int kPro>
+// kX32: fp32 x (XFrag32, the reference's arithmetic); else x rounded to
+// fp16 (XFrag, dot2 arithmetic).
+template <int DT, int kPPT, int kRows, int kWaves, bool kMulti, int kPro, bool kX32>
 __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const float *__restrict__ x,
                                                            Pro pro, int ipr, size_t row_bytes,
                                                            int n_tiles) {
+  using XF = std::conditional_t<kX32, XFrag32<DT>, XFrag<DT>>;
   constexpr int T = 64 * kWaves;
   __shared__ float red[2][kWaves][kRows];
   const int tid = threadIdx.x;
@@ -626,7 +799,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
         g = make_float4(g.x * w.x, g.y * w.y, g.z * w.z, g.w * w.w);
       }
   }
-  XFrag<DT> xf[kPPT];
+  XF xf[kPPT];
 #pragma unroll
   for (int j = 0; j < kPPT; j++) build_xfrag<DT>(xf[j], x4[j], valid[j]);
   float out_scale = 1.0f;
@@ -700,7 +873,7 @@ const Tuning &tuning() {
   return t;
 }
 
-template <int DT, int kPPT, int kRows, int kWaves, int kPro>
+template <int DT, int kPPT, int kRows, int kWaves, int kPro, bool kX32>
 int launch_items(const MatSet &ms, const float *x, const Pro &pro, int n_cols, hipStream_t s) {
   const int ipr = n_cols / 64;
   if (ipr > kPPT * 64 * kWaves) return SWAMP_ESHAPE;
@@ -710,12 +883,12 @@ int launch_items(const MatSet &ms, const float *x, const Pro &pro, int n_cols, h
   if (grid > n_tiles) grid = n_tiles;
   if (grid < 1) return SWAMP_OK;
   if (ms.n == 1)
-    gemv_kernel<DT, kPPT, kRows, kWaves, false, kPro>
+    gemv_kernel<DT, kPPT, kRows, kWaves, false, kPro, kX32>
         <<<grid, 64 * kWaves, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
   else if constexpr (kPro == kProSwiGLU || kPro == kProSwiGLUAcc)
     return SWAMP_EINVAL;  // single matrix only
   else
-    gemv_kernel<DT, kPPT, kRows, kWaves, true, kPro>
+    gemv_kernel<DT, kPPT, kRows, kWaves, true, kPro, kX32>
         <<<grid, 64 * kWaves, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
@@ -742,12 +915,14 @@ int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 
 // several items (rows of more than 512 items); Q6_K capped lower.  Longer tile runs per wave
 // hide the first tile's latency and the x prologue; shorter tiles keep
 // small matrices spread over the whole chip.
-int tile_rows_for(uint32_t dt, int n_cols, int total_rows) {
+int tile_rows_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   const int ipr = n_cols / 64;
   int cap = ipr <= 512 ? 4 : 1;
   // Q6_K items carry twice the decode work: 2-row tiles measure fastest, and
   // 1-row tiles for 8-wave workgroups (n_cols > 16384)
   if (dt == SWAMP_Q6_K) cap = ipr <= 256 ? 2 : 1;
+  // Q8_0 with fp32 x: the register budget allows 2 rows
+  if (dt == SWAMP_Q8_0 && x32) cap = std::min(cap, 2);
   if (tuning().rows) return std::min(tuning().rows, cap);
   const int cus = swamp::device_info().num_cus;
   const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(ipr));
@@ -757,41 +932,48 @@ int tile_rows_for(uint32_t dt, int n_cols, int total_rows) {
   return std::min(r, cap);
 }
 
-template <int DT, int kRows, int kPro>
+template <int DT, int kRows, int kPro, bool kX32>
 int launch_rows(const MatSet &ms, const float *x, const Pro &pro, int n_cols, hipStream_t s) {
   const int ipr = n_cols / 64;
-  if (ipr <= 64) return launch_items<DT, 1, kRows, 1, kPro>(ms, x, pro, n_cols, s);
-  if (ipr <= 128) return launch_items<DT, 1, kRows, 2, kPro>(ms, x, pro, n_cols, s);
-  if (ipr <= 256) return launch_items<DT, 1, kRows, 4, kPro>(ms, x, pro, n_cols, s);
-  if (ipr <= 512) return launch_items<DT, 1, kRows, 8, kPro>(ms, x, pro, n_cols, s);
-  // the fused prologues keep one item per lane (n_cols <= 32768)
-  if constexpr (kPro != kProNone) return SWAMP_ESHAPE;
-  // With two items per lane the tiles are single rows (tile_rows_for caps
-  // them) so both register buffers fit without spills; longer rows take
-  // the generic kernels (item_path_ok).
-  else if constexpr (kRows > 1) return SWAMP_ESHAPE;
-  else if (ipr <= 1024) return launch_items<DT, 2, 1, 8, kPro>(ms, x, pro, n_cols, s);
-  return SWAMP_ESHAPE;
-}
-
-template <int DT, int kPro>
-int launch_dt(const MatSet &ms, const float *x, const Pro &pro, int n_cols, int tile_rows,
-              hipStream_t s) {
-  switch (tile_rows) {
-  case 4: return launch_rows<DT, 4, kPro>(ms, x, pro, n_cols, s);
-  case 2: return launch_rows<DT, 2, kPro>(ms, x, pro, n_cols, s);
-  default: return launch_rows<DT, 1, kPro>(ms, x, pro, n_cols, s);
+  // tiles of at most 2 rows (tile_rows_for): Q6_K always, Q8_0 with fp32 x
+  // (4 double-buffered rows of 68-byte items beside 64 fp32 x values do not
+  // fit 256 VGPRs)
+  if constexpr (kRows > 2 && (DT == SWAMP_Q6_K || (kX32 && DT == SWAMP_Q8_0))) {
+    return SWAMP_ESHAPE;
+  } else {
+    if (ipr <= 64) return launch_items<DT, 1, kRows, 1, kPro, kX32>(ms, x, pro, n_cols, s);
+    if (ipr <= 128) return launch_items<DT, 1, kRows, 2, kPro, kX32>(ms, x, pro, n_cols, s);
+    if (ipr <= 256) return launch_items<DT, 1, kRows, 4, kPro, kX32>(ms, x, pro, n_cols, s);
+    if (ipr <= 512) return launch_items<DT, 1, kRows, 8, kPro, kX32>(ms, x, pro, n_cols, s);
+    // the fused prologues keep one item per lane (n_cols <= 32768)
+    if constexpr (kPro != kProNone) return SWAMP_ESHAPE;
+    // With two items per lane the tiles are single rows (tile_rows_for caps
+    // them) so both register buffers fit without spills; longer rows take
+    // the generic kernels (item_path_ok).
+    else if constexpr (kRows > 1) return SWAMP_ESHAPE;
+    else if (ipr <= 1024) return launch_items<DT, 2, 1, 8, kPro, kX32>(ms, x, pro, n_cols, s);
+    return SWAMP_ESHAPE;
   }
 }
 
-template <int kPro>
+template <int DT, int kPro, bool kX32>
+int launch_dt(const MatSet &ms, const float *x, const Pro &pro, int n_cols, int tile_rows,
+              hipStream_t s) {
+  switch (tile_rows) {
+  case 4: return launch_rows<DT, 4, kPro, kX32>(ms, x, pro, n_cols, s);
+  case 2: return launch_rows<DT, 2, kPro, kX32>(ms, x, pro, n_cols, s);
+  default: return launch_rows<DT, 1, kPro, kX32>(ms, x, pro, n_cols, s);
+  }
+}
+
+template <int kPro, bool kX32>
 int dispatch(uint32_t dt, const MatSet &ms, const float *x, const Pro &pro, int n_cols,
              int tile_rows, hipStream_t s) {
   switch (dt) {
-  case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0, kPro>(ms, x, pro, n_cols, tile_rows, s);
-  case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0, kPro>(ms, x, pro, n_cols, tile_rows, s);
-  case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K, kPro>(ms, x, pro, n_cols, tile_rows, s);
-  case SWAMP_Q6_K: return launch_dt<SWAMP_Q6_K, kPro>(ms, x, pro, n_cols, tile_rows, s);
+  case SWAMP_Q4_0: return launch_dt<SWAMP_Q4_0, kPro, kX32>(ms, x, pro, n_cols, tile_rows, s);
+  case SWAMP_Q8_0: return launch_dt<SWAMP_Q8_0, kPro, kX32>(ms, x, pro, n_cols, tile_rows, s);
+  case SWAMP_Q4_K: return launch_dt<SWAMP_Q4_K, kPro, kX32>(ms, x, pro, n_cols, tile_rows, s);
+  case SWAMP_Q6_K: return launch_dt<SWAMP_Q6_K, kPro, kX32>(ms, x, pro, n_cols, tile_rows, s);
   default: return SWAMP_EDTYPE;
   }
 }
@@ -800,7 +982,7 @@ int dispatch(uint32_t dt, const MatSet &ms, const float *x, const Pro &pro, int 
 // the x prologue); a different dtype starts another launch on the same
 // stream.  Shapes the item kernel does not take go to swamp_launch_gemv
 // one matrix at a time (no prologue: the fused forms reject them first).
-template <int kPro>
+template <int kPro, bool kX32>
 int launch_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
                  const int *row_counts, const float *d_x, const Pro &pro, float *const *d_ys,
                  int n_cols, hipStream_t s) {
@@ -835,9 +1017,9 @@ int launch_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
       }
     if (n == 0) continue;
     MatSet ms;
-    const int tr = tile_rows_for(dt, n_cols, total);
+    const int tr = tile_rows_for(dt, n_cols, total, kX32);
     build_matset(ms, n, ws, ys, rows, tr);
-    int rc = dispatch<kPro>(dt, ms, d_x, pro, n_cols, tr, s);
+    int rc = dispatch<kPro, kX32>(dt, ms, d_x, pro, n_cols, tr, s);
     if (rc) return rc;
   }
   return SWAMP_OK;

@@ -21,7 +21,7 @@ int swamp_launch_gemv_rmsnorm(int n_mats, const uint32_t *dtypes, const void *co
   Pro pro;
   pro.x2 = d_norm_w;
   pro.eps = eps;
-  return launch_multi<kProRmsNorm>(n_mats, dtypes, d_ws, row_counts, d_x, pro, d_ys, n_cols, s);
+  return launch_multi<kProRmsNorm, true>(n_mats, dtypes, d_ws, row_counts, d_x, pro, d_ys, n_cols, s);
 }
 
 int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w, const float *d_gate,
@@ -32,10 +32,10 @@ int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w, const float *d_gat
   MatSet ms;
   const void *ws[1] = {d_w};
   float *ys[1] = {d_y};
-  const int tr = tile_rows_for(dtype, n_cols, n_rows);
+  const int tr = tile_rows_for(dtype, n_cols, n_rows, true);
   build_matset(ms, 1, ws, ys, &n_rows, tr);
   Pro pro;
   pro.x2 = d_up;
-  if (accumulate) return dispatch<kProSwiGLUAcc>(dtype, ms, d_gate, pro, n_cols, tr, s);
-  return dispatch<kProSwiGLU>(dtype, ms, d_gate, pro, n_cols, tr, s);
+  if (accumulate) return dispatch<kProSwiGLUAcc, true>(dtype, ms, d_gate, pro, n_cols, tr, s);
+  return dispatch<kProSwiGLU, true>(dtype, ms, d_gate, pro, n_cols, tr, s);
 }

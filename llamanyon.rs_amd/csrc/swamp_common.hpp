@@ -116,6 +116,8 @@ int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
                          size_t n, hipStream_t s);
 int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x,
                       float *d_y, int n_rows, int n_cols, hipStream_t s);
+int swamp_launch_gemv_f16x(uint32_t dtype, const void *d_w, const float *d_x,
+                           float *d_y, int n_rows, int n_cols, hipStream_t s);
 int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes,
                             const void *const *d_ws, const int *row_counts,
                             const float *d_x, float *const *d_ys, int n_cols,

@@ -27,7 +27,7 @@ TOL = 1e-3
 #   small batch (2..16 tokens), x rounded to fp16 (2^-11 relative);
 #   GEMM, x and the dequantized weights rounded to bf16 (2^-8 relative each);
 #   int8 GEMM, x quantized to Q8_0 (the oracle multiplies the same Q8_0 x).
-BOUND = {"gemv": 1e-3, "batched_f16": 1e-4, "gemm_bf16": 4e-4, "gemm_i8": 1e-5}
+BOUND = {"gemv": 1e-6, "batched_f16": 1e-4, "gemm_bf16": 4e-4, "gemm_i8": 1e-5}
 
 LLAMA8B = {"qkv": (6144, 4096), "o_proj": (4096, 4096), "gate_up": (28672, 4096),
            "down": (4096, 14336), "lm_head": (128256, 4096)}
@@ -118,6 +118,32 @@ def test_config_decode_gemv(pkg, orc, torch_dev, W, errlog, model, name, dtype, 
     err = errlog(f"gemv {model} {name}", check_rows(pkg, orc, dtype, raw, cols, y, x, rows),
                  path="gemv")
     assert err <= min(TOL, BOUND["gemv"])
+
+
+@pytest.mark.parametrize("name", ["qkv", "gate_up", "lm_head"])
+@pytest.mark.parametrize("dtype", [Q4_0, Q4_K, Q8_0])
+def test_gemv_fp32_gate_rejects_fp16_x(pkg, orc, torch_dev, W, errlog, dtype, name):
+    """The GEMV gate (1e-6) is tight enough that rounding x to fp16 fails
+    it: swamp_qgemv (fp32 x) passes it, swamp_qgemv_f16x (x rounded to
+    fp16 inside the kernel) stays within the 1e-3 contract but not within
+    1e-6, on the same inputs."""
+    torch = torch_dev
+    rows, cols = LLAMA8B[name]
+    raw, d_w = W.get(dtype, rows, cols, 0.02)
+    x = pkg.fill_normal(0xA11CE ^ 0xF16 ^ rows, 1.0, 1, cols)
+    print(f"[gpu case] fp32 gate vs fp16 x {name} dtype {dtype}", flush=True)
+    d_x = torch.from_numpy(x[0]).cuda()
+    errs = []
+    for fn in (pkg.qgemv, pkg.qgemv_f16x):
+        d_y = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+        fn(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), rows, cols,
+           stream(torch))
+        torch.cuda.synchronize()
+        errs.append(check_rows(pkg, orc, dtype, raw, cols, d_y.cpu().numpy()[None, :], x, rows))
+    errlog(f"gemv 8b {name} dtype={dtype} fp32 x", errs[0], path="gemv")
+    errlog(f"gemv 8b {name} dtype={dtype} fp16 x", errs[1], path="gemv_f16x")
+    assert errs[0] <= BOUND["gemv"]
+    assert BOUND["gemv"] < errs[1] <= TOL
 
 
 # ------------------------------------------------------------ small batch

@@ -14,7 +14,10 @@
  *  - y[r] = sum_k W[r,k] * x[k] in fp32.
  *  - Pointers named d_* are DEVICE pointers; the caller owns every buffer.
  *  - stream is a hipStream_t passed as void* (NULL = default stream); every
- *    device entry point is asynchronous on it and allocates nothing.
+ *    device entry point is asynchronous on it.  None allocates, except that
+ *    swamp_qgemv_batched and swamp_qgemm take scratch memory for split
+ *    reductions from a buffer the library keeps per (device, stream): see
+ *    "Scratch" below.
  *  - Return 0 on success, a negative SWAMP_E* code on error; on error no
  *    output is written and nothing is launched.
  */
@@ -155,9 +158,11 @@ SWAMP_API int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
  * 16 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass of one token
  * runs the decode GEMV, and n_tok > 16 runs swamp_qgemm's kernels on x
- * rounded to bf16 (kept in a per-(device, stream) buffer the library
- * allocates on first use).  The 2..16-token kernel rounds x to fp16:
- * entries must lie within its range (|x| < 65504).  Q6_K:
+ * rounded to bf16 (in scratch; without scratch, passes of 16 instead).
+ * Passes of 2..16 tokens round x to fp16 on the matrix cores (about 3e-5
+ * of ||W_r|| ||x|| against the fp32 reference; more than 16 tokens, bf16:
+ * about 1e-4): entries must lie within fp16 range (|x| < 65504), also for
+ * accumulate = 1 and when no scratch is available.  Q6_K:
  * forward_linear_batch sends it to fallback_gemv (linear.rs:336-364), the
  * GEMV per token written over y;
  * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
@@ -179,12 +184,36 @@ SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     weights only; n_cols a multiple of 128.
  * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only; Q6_K -> SWAMP_EDTYPE);
  * bf16 x needs n_cols a multiple of 64.  When the tiles do not fill the
- * GPU, K is split across workgroups whose partial tiles go to a scratch
- * buffer the library keeps per (device, stream), summed in piece order by
- * a second kernel (deterministic); calls on one stream share it. */
+ * GPU, K is split across workgroups whose partial tiles go to scratch and
+ * are summed in piece order by a second kernel (deterministic). */
 SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);
+
+/* Scratch.  swamp_qgemv_batched and swamp_qgemm need scratch memory for
+ * some shapes (the partial sums of K split across workgroups, and the bf16
+ * copy of x of a batch of more than 16 tokens).  The library keeps one
+ * buffer per (device, stream) for it (hipStreamPerThread: per host thread
+ * too), allocated on first use and replaced when a call needs more, both
+ * stream-ordered on that stream (hipMallocAsync / hipFreeAsync): no call
+ * synchronizes the host.  While the stream is being captured into a graph
+ * nothing is allocated: a call that needs more than the stream's buffer
+ * holds takes the path without scratch (split pieces added with float
+ * atomics into y cleared by a kernel, which is not bit-reproducible; more
+ * than 16 tokens in passes of 16).  Calls on one stream must be issued from
+ * one host thread at a time: two threads calling on the same stream (the
+ * null stream included) at once race on its buffer.
+ *   swamp_qgemv_batched_workspace / swamp_qgemm_workspace: the scratch
+ *     bytes such a call takes (0: none);
+ *   swamp_workspace_reserve: make the stream's buffer at least `bytes`
+ *     long now (for example before capturing calls into a graph); 0, or
+ *     SWAMP_EWORKSPACE when it cannot be allocated or the stream is being
+ *     captured. */
+SWAMP_API size_t swamp_qgemv_batched_workspace(uint32_t dtype, int n_tok, int n_rows,
+                                               int n_cols, int accumulate);
+SWAMP_API size_t swamp_qgemm_workspace(uint32_t dtype, uint32_t x_type, int m, int n_rows,
+                                       int n_cols);
+SWAMP_API int swamp_workspace_reserve(void *stream, size_t bytes);
 
 /* Activation producers for the small batch (out_type SWAMP_F32) and the
  * prefill GEMM (SWAMP_BF16: its bf16 x, rounded to nearest even), over

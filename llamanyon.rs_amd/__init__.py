@@ -41,6 +41,7 @@ GPU_SYMBOLS = (
     "swamp_qgemv_rmsnorm", "swamp_qgemv_swiglu",
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
     "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
+    "swamp_qgemv_batched_workspace", "swamp_qgemm_workspace", "swamp_workspace_reserve",
 )
 # Every symbol include/swamp_gguf.h declares (also in libswamp_gpu.so).
 GGUF_SYMBOLS = (
@@ -119,6 +120,9 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_swiglu": (i32, [c_vp, c_vp, c_vp, u32, c_size, c_vp]),
         "swamp_quantize_q8_0": (i32, [c_vp, u32, c_vp, c_size, c_vp]),
         "swamp_fused_gemv_q4k": (None, [c_vp, c_vp, c_vp, i32, i32]),
+        "swamp_qgemv_batched_workspace": (c_size, [u32, i32, i32, i32, i32]),
+        "swamp_qgemm_workspace": (c_size, [u32, u32, i32, i32, i32]),
+        "swamp_workspace_reserve": (i32, [c_vp, c_size]),
         "swamp_gemv_q8_vnni": (ctypes.c_float, [c_vp, c_vp, i32, ctypes.c_float]),
         # GGUF reader (include/swamp_gguf.h)
         "swamp_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(c_vp)]),
@@ -286,6 +290,11 @@ def rmsnorm_rows(d_x: int, d_norm_w: int, eps: float, d_out: int, out_type: int,
 def swiglu(d_gate: int, d_up: int, d_out: int, out_type: int, n: int, stream: int = 0) -> None:
     """silu(gate) * up (ops.rs:203-214) into fp32 or bf16."""
     _check(gpu_lib().swamp_swiglu(d_gate, d_up, d_out, out_type, n, stream), "swamp_swiglu")
+
+
+def workspace_reserve(stream: int, n_bytes: int) -> None:
+    """Make the stream's scratch buffer at least n_bytes long now."""
+    _check(gpu_lib().swamp_workspace_reserve(stream, n_bytes), "swamp_workspace_reserve")
 
 
 def quantize_q8_0(d_x: int, x_type: int, d_q: int, n: int, stream: int = 0) -> None:

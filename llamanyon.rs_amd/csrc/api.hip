@@ -7,8 +7,8 @@
 // codes, checked before anything is launched; the two legacy host-pointer
 // exports keep their silent-return behaviour.
 #include <algorithm>
-#include <atomic>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "swamp_common.hpp"
@@ -103,11 +103,11 @@ const DeviceInfo &device_info() {
   return g_info[dev];
 }
 
-void *stream_workspace(hipStream_t s, size_t bytes, int slot) {
+void *stream_workspace(hipStream_t s, size_t bytes) {
   struct Entry {
     int dev;
     hipStream_t s;
-    int slot;
+    std::thread::id tid;  // for hipStreamPerThread, one stream per host thread
     void *p;
     size_t bytes;
   };
@@ -115,21 +115,29 @@ void *stream_workspace(hipStream_t s, size_t bytes, int slot) {
   static std::vector<Entry> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const std::thread::id tid =
+      s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
   std::lock_guard<std::mutex> lock(mu);
-  for (Entry &e : cache) {
-    if (e.dev != dev || e.s != s || e.slot != slot) continue;
-    if (e.bytes >= bytes) return e.p;
-    if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
-    (void)hipFree(e.p);
-    e.p = nullptr;
-    e.bytes = 0;
-    if (hipMalloc(&e.p, bytes) != hipSuccess) return e.p = nullptr;
-    e.bytes = bytes;
-    return e.p;
-  }
+  Entry *e = nullptr;
+  for (Entry &c : cache)
+    if (c.dev == dev && c.s == s && c.tid == tid) e = &c;
+  if (e && e->bytes >= bytes) return e->p;
+  // a (larger) buffer is needed: never while the stream is being captured
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+    return nullptr;
   void *p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-  cache.push_back(Entry{dev, s, slot, p, bytes});
+  if (hipMallocAsync(&p, bytes, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (e) {
+    (void)hipFreeAsync(e->p, s);  // after the work already queued on s
+    e->p = p;
+    e->bytes = bytes;
+  } else {
+    cache.push_back(Entry{dev, s, tid, p, bytes});
+  }
   return p;
 }
 
@@ -313,12 +321,12 @@ int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len, const flo
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (dtype != SWAMP_Q4_K && n_cols % 64 != 0) return SWAMP_ESHAPE;
   if (int rc = ensure_device(nullptr)) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   if (n_cols == 0)
-    return accumulate ? SWAMP_OK
-                      : fill_zero(d_y, size_t(n_tok) * size_t(n_rows),
-                                  static_cast<hipStream_t>(stream));
-  return swamp_launch_gemv_batched(dtype, d_w, d_x, d_y, n_tok, n_rows, n_cols, accumulate ? 1 : 0,
-                                   static_cast<hipStream_t>(stream));
+    return accumulate ? SWAMP_OK : fill_zero(d_y, size_t(n_tok) * size_t(n_rows), s);
+  const int acc = accumulate ? 1 : 0;
+  Scratch sc = stream_scratch(s, swamp_batched_scratch_bytes(dtype, n_tok, n_rows, n_cols, acc));
+  return swamp_launch_gemv_batched(dtype, d_w, d_x, d_y, n_tok, n_rows, n_cols, acc, sc, s);
 }
 
 int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, uint32_t x_type,
@@ -332,10 +340,27 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;
   if (int rc = ensure_device(nullptr)) return rc;
-  if (n_cols == 0)
-    return fill_zero(d_y, size_t(m) * size_t(n_rows), static_cast<hipStream_t>(stream));
-  return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols,
-                           static_cast<hipStream_t>(stream));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_cols == 0) return fill_zero(d_y, size_t(m) * size_t(n_rows), s);
+  Scratch sc = stream_scratch(s, swamp_gemm_scratch_bytes(dtype, x_type, m, n_rows, n_cols));
+  return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols, sc, s);
+}
+
+size_t swamp_qgemv_batched_workspace(uint32_t dtype, int n_tok, int n_rows, int n_cols,
+                                     int accumulate) {
+  if (ensure_device(nullptr) != SWAMP_OK) return 0;
+  return swamp_batched_scratch_bytes(dtype, n_tok, n_rows, n_cols, accumulate ? 1 : 0);
+}
+
+size_t swamp_qgemm_workspace(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols) {
+  if (ensure_device(nullptr) != SWAMP_OK) return 0;
+  return swamp_gemm_scratch_bytes(dtype, x_type, m, n_rows, n_cols);
+}
+
+int swamp_workspace_reserve(void *stream, size_t bytes) {
+  if (int rc = ensure_device(nullptr)) return rc;
+  if (bytes == 0) return SWAMP_OK;
+  return stream_workspace(static_cast<hipStream_t>(stream), bytes) ? SWAMP_OK : SWAMP_EWORKSPACE;
 }
 
 int swamp_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps, void *d_out,

@@ -566,9 +566,31 @@ int launch_tiles(const uint8_t *w, const uint16_t *x, float *y, int m, int n_row
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
 
+// Work decomposition of one bf16 GEMM call (the choice follows measured
+// step times of one tile on one CU -- full 2.0 us, half 1.3 us at 8B
+// shapes -- and 6 TB/s for the partial sums: written, read, y written).
+//  kSmall  at most 64 tokens: 64-token tiles (a quarter of the MFMA work of
+//          a full tile for the same weight stream), split along K into up
+//          to 8 pieces while they fill at most half the CUs;
+//  kSplit  at most half a round of tiles: full tiles split along K into up
+//          to 8 pieces, or 128-token halves (split into up to 4 pieces when
+//          they fill at most half the CUs);
+//  kRounds full tiles in complete rounds, a last round at most half full as
+//          128-token halves (no partial sums).
+// Split pieces write partial tiles to scratch, summed in piece order by a
+// second kernel (deterministic).  Without scratch the pieces add into
+// zeroed y with float atomics (and kSplit takes halves).
+struct GemmPlan {
+  enum Kind { kSmall, kSplit, kRounds } kind;
+  bool full;      // kSplit: full tiles (else halves)
+  int pieces;     // K pieces (1: none)
+  int kps;        // K steps per piece
+  int half_pieces, half_kps;  // kSplit fallback without scratch: halves
+  size_t part_bytes;          // scratch for the pieces' partial sums
+};
+
 template <int DT>
-int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows, int n_cols,
-                hipStream_t s) {
+GemmPlan plan_bf16(int m, int n_rows, int n_cols) {
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n, KT = n_cols / kBK;
   const int cus = swamp::device_info().num_cus;
@@ -578,68 +600,69 @@ int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows
     if (DT == SWAMP_Q4_K) kps = (kps + 3) / 4 * 4;
     return kps;
   };
-  // At most half a round of tiles: either full tiles split along K into up
-  // to 8 pieces, or 128-token halves (split into up to 4 pieces when they
-  // fill at most half the CUs).  Split pieces write partial tiles to the
-  // stream's workspace, summed in piece order by a second kernel
-  // (deterministic); without a workspace, halves whose pieces add into
-  // zeroed y with float atomics.  The choice follows measured step times of
-  // one tile on one CU (full 2.0 us, half 1.3 us at 8B shapes) and 6 TB/s
-  // for the partial sums (written, read, y written).
-  // At most 64 tokens: 64-token tiles (a quarter of the MFMA work of a
-  // full tile for the same weight stream), split along K while they fill
-  // at most half the CUs.
+  GemmPlan p{GemmPlan::kRounds, true, 1, KT, 1, KT, 0};
   if (m <= kBM / 4) {
+    p.kind = GemmPlan::kSmall;
     int pieces = 2 * tiles <= cus ? std::max(1, std::min({cus / tiles, 8, KT / 8})) : 1;
-    const int kps = piece_len(pieces);
-    pieces = (KT + kps - 1) / kps;
-    float *part = nullptr;
-    if (pieces > 1)
-      part = static_cast<float *>(swamp::stream_workspace(s, size_t(pieces) * mn * sizeof(float)));
-    if (pieces > 1 && !part)
-      zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
-    const Work wk{tiles_m, tiles_n, 0, 1, pieces, kps, part};
-    if (int rc = launch_tiles<DT, 2>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
-    if (pieces > 1 && part) {
-      split_reduce_kernel<<<unsigned((mn + 255) / 256), 256, 0, s>>>(part, y, pieces, mn);
-      if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
-    }
-    return SWAMP_OK;
-  }
-  if (2 * tiles <= cus) {
+    p.kps = piece_len(pieces);
+    p.pieces = (KT + p.kps - 1) / p.kps;
+  } else if (2 * tiles <= cus) {
+    p.kind = GemmPlan::kSplit;
     auto est_us = [&](double step_us, int pieces) {
       double t_us = double(piece_len(pieces)) * step_us;
       if (pieces > 1) t_us += (2.0 * pieces + 1.0) * double(mn) * 4.0 / 6e6;
       return t_us;
     };
-    int fs = std::min({cus / tiles, 8, KT / 8});
-    int hs = 4 * tiles <= cus ? std::max(1, std::min({cus / (2 * tiles), 4, KT / 8})) : 1;
-    const bool full = fs >= 2 && est_us(2.0, fs) < est_us(1.3, hs);
-    int pieces = full ? fs : hs;
-    const int kps = piece_len(pieces);
-    pieces = (KT + kps - 1) / kps;
-    float *part = nullptr;
-    if (pieces > 1)
-      part = static_cast<float *>(swamp::stream_workspace(s, size_t(pieces) * mn * sizeof(float)));
-    if (full && !part) {  // no workspace: halves instead
-      pieces = hs;
-      const int hk = piece_len(pieces);
-      pieces = (KT + hk - 1) / hk;
-    }
-    if (full && part) {
-      const Work wk{tiles_m, tiles_n, 0, 1, pieces, kps, part};
-      if (int rc = launch_tiles<DT, 8>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    const int fs = std::min({cus / tiles, 8, KT / 8});
+    const int hs = 4 * tiles <= cus ? std::max(1, std::min({cus / (2 * tiles), 4, KT / 8})) : 1;
+    p.half_kps = piece_len(hs);
+    p.half_pieces = (KT + p.half_kps - 1) / p.half_kps;
+    p.full = fs >= 2 && est_us(2.0, fs) < est_us(1.3, hs);
+    if (p.full) {
+      p.kps = piece_len(fs);
+      p.pieces = (KT + p.kps - 1) / p.kps;
     } else {
-      const int hk = piece_len(pieces);
-      if (pieces > 1 && !part)
-        zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
-      const Work wk{tiles_m, tiles_n, 0, 2, pieces, hk, pieces > 1 ? part : nullptr};
-      if (int rc = launch_tiles<DT, 4>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+      p.kps = p.half_kps;
+      p.pieces = p.half_pieces;
     }
-    if (pieces > 1 && part) {
-      split_reduce_kernel<<<unsigned((mn + 255) / 256), 256, 0, s>>>(part, y, pieces, mn);
-      if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+  }
+  p.part_bytes = p.pieces > 1 ? size_t(p.pieces) * mn * sizeof(float) : 0;
+  return p;
+}
+
+template <int DT>
+int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows, int n_cols,
+                swamp::Scratch &sc, hipStream_t s) {
+  const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
+  const int tiles = tiles_m * tiles_n, KT = n_cols / kBK;
+  const int cus = swamp::device_info().num_cus;
+  const size_t mn = size_t(m) * size_t(n_rows);
+  const GemmPlan p = plan_bf16<DT>(m, n_rows, n_cols);
+  float *part = p.part_bytes ? static_cast<float *>(sc.get(p.part_bytes)) : nullptr;
+  if (p.kind == GemmPlan::kSmall) {
+    if (p.pieces > 1 && !part)
+      zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
+    const Work wk{tiles_m, tiles_n, 0, 1, p.pieces, p.kps, part};
+    if (int rc = launch_tiles<DT, 2>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    if (p.pieces > 1 && part) return swamp_launch_split_reduce(part, y, p.pieces, mn, s);
+    return SWAMP_OK;
+  }
+  if (p.kind == GemmPlan::kSplit) {
+    if (p.full && part) {
+      const Work wk{tiles_m, tiles_n, 0, 1, p.pieces, p.kps, part};
+      if (int rc = launch_tiles<DT, 8>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+      return swamp_launch_split_reduce(part, y, p.pieces, mn, s);
     }
+    // halves: their pieces go to scratch when it is there, else add into
+    // zeroed y
+    const bool use_part = !p.full && part;
+    const int pieces = p.full ? p.half_pieces : p.pieces;
+    const int kps = p.full ? p.half_kps : p.kps;
+    if (pieces > 1 && !use_part)
+      zero_tiles_kernel<<<unsigned(tiles * 64), 256, 0, s>>>(y, m, n_rows, tiles_m, tiles_n, 0);
+    const Work wk{tiles_m, tiles_n, 0, 2, pieces, kps, use_part ? part : nullptr};
+    if (int rc = launch_tiles<DT, 4>(w, x, y, m, n_rows, n_cols, wk, tiles, s)) return rc;
+    if (pieces > 1 && use_part) return swamp_launch_split_reduce(part, y, pieces, mn, s);
     return SWAMP_OK;
   }
   // Full tiles in complete rounds; a last round at most half full as
@@ -663,10 +686,31 @@ int launch_bf16(const uint8_t *w, const uint16_t *x, float *y, int m, int n_rows
 
 }  // namespace
 
+int swamp_launch_split_reduce(const float *d_part, float *d_y, int pieces, size_t n,
+                              hipStream_t s) {
+  if (pieces < 1 || pieces > 8) return SWAMP_EINVAL;
+  split_reduce_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(d_part, d_y, pieces, n);
+  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+}
+
+size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols) {
+  if (m <= 0 || n_rows <= 0 || n_cols <= 0) return 0;
+  if (x_type == SWAMP_Q8_0) return swamp_gemm_i8_scratch_bytes(dtype, m, n_rows, n_cols);
+  if (x_type != SWAMP_BF16 || n_cols % kBK != 0) return 0;
+  switch (dtype) {
+    case SWAMP_Q4_0: return plan_bf16<SWAMP_Q4_0>(m, n_rows, n_cols).part_bytes;
+    case SWAMP_Q8_0: return plan_bf16<SWAMP_Q8_0>(m, n_rows, n_cols).part_bytes;
+    case SWAMP_Q4_K: return plan_bf16<SWAMP_Q4_K>(m, n_rows, n_cols).part_bytes;
+    default: return 0;
+  }
+}
+
 int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t x_type,
-                      float *d_y, int m, int n_rows, int n_cols, hipStream_t s) {
+                      float *d_y, int m, int n_rows, int n_cols, swamp::Scratch &sc,
+                      hipStream_t s) {
   if (m == 0 || n_rows == 0) return SWAMP_OK;
-  if (x_type == SWAMP_Q8_0) return swamp_launch_gemm_i8(dtype, d_w, d_x, d_y, m, n_rows, n_cols, s);
+  if (x_type == SWAMP_Q8_0)
+    return swamp_launch_gemm_i8(dtype, d_w, d_x, d_y, m, n_rows, n_cols, sc, s);
   if (x_type != SWAMP_BF16) return SWAMP_EDTYPE;
   if (n_cols % kBK != 0) return SWAMP_ESHAPE;
   // activation offsets are 32-bit (buffer descriptors)
@@ -674,9 +718,9 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint16_t *x = static_cast<const uint16_t *>(d_x);
   switch (dtype) {
-    case SWAMP_Q4_0: return launch_bf16<SWAMP_Q4_0>(w, x, d_y, m, n_rows, n_cols, s);
-    case SWAMP_Q8_0: return launch_bf16<SWAMP_Q8_0>(w, x, d_y, m, n_rows, n_cols, s);
-    case SWAMP_Q4_K: return launch_bf16<SWAMP_Q4_K>(w, x, d_y, m, n_rows, n_cols, s);
+    case SWAMP_Q4_0: return launch_bf16<SWAMP_Q4_0>(w, x, d_y, m, n_rows, n_cols, sc, s);
+    case SWAMP_Q8_0: return launch_bf16<SWAMP_Q8_0>(w, x, d_y, m, n_rows, n_cols, sc, s);
+    case SWAMP_Q4_K: return launch_bf16<SWAMP_Q4_K>(w, x, d_y, m, n_rows, n_cols, sc, s);
     default: return SWAMP_EDTYPE;
   }
 }

@@ -195,7 +195,8 @@ __device__ __forceinline__ void compute(f32x16_t (&acc)[2][2], const uint8_t *st
 template <int DT>
 __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
     const uint8_t *__restrict__ w, const uint8_t *__restrict__ xq8, float *__restrict__ y, int M,
-    int N, int K, size_t row_bytes, int tiles_m, int tiles_n, int kt_per_split, int atomic) {
+    int N, int K, size_t row_bytes, int tiles_m, int tiles_n, int kt_per_split, int atomic,
+    float *__restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -257,7 +258,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
         const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * fc + (e & 3);
         if (m < M && n < N) {
           float *dst = y + size_t(m) * N + n;
-          if (atomic) unsafeAtomicAdd(dst, acc[i][j][e]);
+          if (part) part[(size_t(split) * M + m) * N + n] = acc[i][j][e];
+          else if (atomic) unsafeAtomicAdd(dst, acc[i][j][e]);
           else *dst = acc[i][j][e];
         }
       }
@@ -282,25 +284,48 @@ int set_smem_attr_i8() {
 
 }  // namespace
 
+namespace {
+
+// K splits of an int8 GEMM call: two workgroups fit per CU (72 KB LDS
+// each); when the tiles do not fill them, K is split into up to 8 pieces.
+void plan_i8(int m, int n_rows, int n_cols, int &splits, int &kt_per_split) {
+  const int tiles = ((m + kBM - 1) / kBM) * ((n_rows + kBN - 1) / kBN);
+  const int KT = n_cols / (32 * kBlk);
+  const int cus = swamp::device_info().num_cus;
+  splits = std::max(1, std::min({2 * cus / std::max(1, tiles), KT / 4, 8}));
+  kt_per_split = (KT + splits - 1) / splits;
+  splits = (KT + kt_per_split - 1) / kt_per_split;
+}
+
+}  // namespace
+
+size_t swamp_gemm_i8_scratch_bytes(uint32_t dtype, int m, int n_rows, int n_cols) {
+  if (m <= 0 || n_rows <= 0 || n_cols % (32 * kBlk) != 0) return 0;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0) return 0;
+  int splits, kps;
+  plan_i8(m, n_rows, n_cols, splits, kps);
+  return splits > 1 ? size_t(splits) * size_t(m) * size_t(n_rows) * sizeof(float) : 0;
+}
+
 int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, float *d_y, int m,
-                         int n_rows, int n_cols, hipStream_t s) {
+                         int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s) {
   if (m == 0 || n_rows == 0) return SWAMP_OK;
   if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0) return SWAMP_EDTYPE;
   if (n_cols % (32 * kBlk) != 0) return SWAMP_ESHAPE;
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n;
-  const int KT = n_cols / (32 * kBlk);
   const int cus = swamp::device_info().num_cus;
-  // two workgroups fit per CU (72 KB LDS each)
-  int splits = std::max(1, std::min(2 * cus / std::max(1, tiles), KT / 4));
-  const int kt_per_split = (KT + splits - 1) / splits;
-  splits = (KT + kt_per_split - 1) / kt_per_split;
-  const int atomic = splits > 1 ? 1 : 0;
-  if (atomic) {
-    const size_t n = size_t(m) * n_rows;
+  int splits, kt_per_split;
+  plan_i8(m, n_rows, n_cols, splits, kt_per_split);
+  // split pieces go to scratch and are summed in piece order (deterministic);
+  // without scratch they add into zeroed y with float atomics
+  const size_t n = size_t(m) * n_rows;
+  float *part = splits > 1 ? static_cast<float *>(sc.get(size_t(splits) * n * sizeof(float)))
+                           : nullptr;
+  const int atomic = splits > 1 && !part ? 1 : 0;
+  if (atomic)
     zero_f32_i8_kernel<<<unsigned(std::min<size_t>((n + 255) / 256, size_t(cus) * 16)), 256, 0,
                          s>>>(d_y, n);
-  }
   const dim3 grid{unsigned(tiles), unsigned(splits), 1u};
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint8_t *x = static_cast<const uint8_t *>(d_xq8);
@@ -308,11 +333,13 @@ int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, flo
   if (dtype == SWAMP_Q4_0) {
     if (int rc = set_smem_attr_i8<SWAMP_Q4_0>()) return rc;
     gemm_i8_kernel<SWAMP_Q4_0><<<grid, kThreads, kSmemBytes, s>>>(
-        w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic);
+        w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic, part);
   } else {
     if (int rc = set_smem_attr_i8<SWAMP_Q8_0>()) return rc;
     gemm_i8_kernel<SWAMP_Q8_0><<<grid, kThreads, kSmemBytes, s>>>(
-        w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic);
+        w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic, part);
   }
-  return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
+  if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
+  if (part) return swamp_launch_split_reduce(part, d_y, splits, n, s);
+  return SWAMP_OK;
 }

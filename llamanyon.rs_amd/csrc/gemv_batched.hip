@@ -655,9 +655,43 @@ int launch_pass(Args a, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+
+// The GEMM route of a call: more than 16 tokens written over y, on x rounded
+// to bf16 (in scratch).
+bool gemm_route(int n_tok, int n_cols, int accumulate) {
+  return n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
+         size_t(n_tok) * size_t(n_cols) * 2 <= size_t(UINT32_MAX);
+}
+
+// Scratch of the small-batch passes: the largest K-group partial block.
+size_t kgroup_bytes(int n_tok, int n_rows, int n_cols, int accumulate) {
+  size_t ws = 0;
+  for (int t0 = 0; t0 < n_tok; t0 += kTok) {
+    const int nt = std::min(kTok, n_tok - t0);
+    if (nt == 1 && !accumulate) continue;  // the decode GEMV
+    const int nkg = pass_kgroups(nt, n_rows, n_cols);
+    if (nkg > 1) ws = std::max(ws, size_t(nkg) * nt * n_rows * sizeof(float));
+  }
+  return ws;
+}
+
+}  // namespace
+
+size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols,
+                                   int accumulate) {
+  if (n_tok <= 0 || n_rows <= 0 || n_cols <= 0) return 0;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return 0;
+  if (gemm_route(n_tok, n_cols, accumulate)) {
+    const size_t xb = (size_t(n_tok) * size_t(n_cols) * 2 + 255) & ~size_t(255);
+    return xb + swamp_gemm_scratch_bytes(dtype, SWAMP_BF16, n_tok, n_rows, n_cols);
+  }
+  return kgroup_bytes(n_tok, n_rows, n_cols, accumulate);
+}
+
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
                               int n_tok, int n_rows, int n_cols, int accumulate,
-                              hipStream_t s) {
+                              swamp::Scratch &sc, hipStream_t s) {
   if (n_rows == 0 || n_tok == 0) return SWAMP_OK;
   if (dtype == SWAMP_Q6_K) {
     // forward_linear_batch sends Q6_K to fallback_gemv (linear.rs:336-364):
@@ -671,18 +705,16 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     return SWAMP_OK;
   }
   // Batches of more than 16 tokens written over y run as the prefill GEMM
-  // on x rounded to bf16 (in the stream's activation workspace): its
-  // 64-token tiles cost less than streaming the weights again per pass of
-  // 16 (8B Q4_0 gate+up at 24 tokens: 36 us against 50 us; at 64: 42 us
-  // against 107 us).  Without the workspace the passes below run instead.
-  if (n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
-      size_t(n_tok) * size_t(n_cols) * 2 <= size_t(UINT32_MAX)) {
+  // on x rounded to bf16 (in scratch): its 64-token tiles cost less than
+  // streaming the weights again per pass of 16 (8B Q4_0 gate+up at 24
+  // tokens: 36 us against 50 us; at 64: 42 us against 107 us).  Without
+  // scratch the passes below run instead.
+  if (gemm_route(n_tok, n_cols, accumulate)) {
     const size_t n = size_t(n_tok) * size_t(n_cols);
-    void *xb = swamp::stream_workspace(s, n * 2, 1);
-    if (xb) {
+    if (void *xb = sc.get(n * 2)) {
       int rc = swamp_launch_f32_to_bf16(d_x, xb, n, s);
       if (rc == SWAMP_OK)
-        rc = swamp_launch_gemm(dtype, d_w, xb, SWAMP_BF16, d_y, n_tok, n_rows, n_cols, s);
+        rc = swamp_launch_gemm(dtype, d_w, xb, SWAMP_BF16, d_y, n_tok, n_rows, n_cols, sc, s);
       return rc;
     }
   }
@@ -696,15 +728,10 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   // 16 rows of a tile are addressed by one buffer descriptor (32-bit range)
   if (size_t(a.row_bytes) * kRowsTile >= (size_t(1) << 30)) return SWAMP_ESHAPE;
   if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return SWAMP_EDTYPE;
-  // workspace for the passes that split K over workgroups
-  size_t ws_bytes = 0;
-  for (int t0 = 0; t0 < n_tok; t0 += kTok) {
-    const int nt = std::min(kTok, n_tok - t0);
-    const int nkg = pass_kgroups(nt, n_rows, n_cols);
-    if (nkg > 1) ws_bytes = std::max(ws_bytes, size_t(nkg) * nt * n_rows * sizeof(float));
-  }
-  // without a workspace the passes run as K phases
-  a.ws = ws_bytes ? static_cast<float *>(swamp::stream_workspace(s, ws_bytes)) : nullptr;
+  // scratch for the passes that split K over workgroups; without it the
+  // passes run as K phases
+  const size_t ws_bytes = kgroup_bytes(n_tok, n_rows, n_cols, accumulate);
+  a.ws = ws_bytes ? static_cast<float *>(sc.get(ws_bytes)) : nullptr;
   int rc = SWAMP_OK;
   for (int t0 = 0; t0 < n_tok && rc == SWAMP_OK; t0 += kTok) {
     a.n_tok = std::min(kTok, n_tok - t0);

@@ -97,15 +97,45 @@ struct DeviceInfo {
 };
 const DeviceInfo &device_info();  // current device (initialises it)
 
-// Scratch memory of at least `bytes` for work queued on stream s of the
-// current device.  One buffer per (device, stream, slot): calls on one
-// stream run in order and may share it, calls on different streams never
-// do; slot 0 holds partial sums of split reductions, slot 1 converted
-// activations (which a call may hold while it uses slot 0).  A buffer
-// grows on demand (after the stream's queued work is done with the old
-// one) and lives until the process exits.  nullptr when it cannot be
-// allocated.
-void *stream_workspace(hipStream_t s, size_t bytes, int slot = 0);
+// Scratch memory of one entry-point call: partial sums of split reductions
+// and converted activations, carved from one region by a bump allocator
+// (256-byte aligned pieces).  The region is either the per-(device,
+// stream) buffer of stream_workspace or a fixed region the caller names.
+// get() returns nullptr once the region is exhausted; every caller then
+// takes its path without scratch.
+struct Scratch {
+  uint8_t *base = nullptr;
+  size_t cap = 0, used = 0;
+  void *get(size_t bytes) {
+    const size_t n = (bytes + 255) & ~size_t(255);
+    if (!base || n > cap - used) return nullptr;
+    void *p = base + used;
+    used += n;
+    return p;
+  }
+};
+
+// The per-(device, stream) buffer, at least `bytes` long, for work queued
+// on stream s of the current device; calls on one stream run in order and
+// share it, calls on different streams never do (hipStreamPerThread is
+// also told apart by host thread).  It is allocated on first use and
+// replaced by a larger one when a call needs more, both stream-ordered on
+// s (hipMallocAsync, the old one released by hipFreeAsync), so no call
+// blocks the host.  While s is being captured into a graph nothing is
+// allocated: nullptr when the buffer is missing or too small.  nullptr also
+// when the allocation fails.
+void *stream_workspace(hipStream_t s, size_t bytes);
+
+// Scratch over the stream's buffer, sized for `bytes` (empty when bytes is
+// 0 or the buffer is not available).
+inline Scratch stream_scratch(hipStream_t s, size_t bytes) {
+  Scratch sc;
+  if (bytes) {
+    sc.base = static_cast<uint8_t *>(stream_workspace(s, bytes));
+    sc.cap = sc.base ? bytes : 0;
+  }
+  return sc;
+}
 
 }  // namespace swamp
 
@@ -130,15 +160,23 @@ int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w,
                              const float *d_gate, const float *d_up, float *d_y,
                              int n_rows, int n_cols, int accumulate,
                              hipStream_t s);
+// Scratch bytes a call will take from its region (0: none), from the same
+// plans the launchers follow.
+size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols,
+                                   int accumulate);
+size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols);
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,
                               const float *d_x, float *d_y, int n_tok,
                               int n_rows, int n_cols, int accumulate,
-                              hipStream_t s);
+                              swamp::Scratch &sc, hipStream_t s);
 int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x,
                       uint32_t x_type, float *d_y, int m, int n_rows,
-                      int n_cols, hipStream_t s);
+                      int n_cols, swamp::Scratch &sc, hipStream_t s);
 int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, float *d_y, int m,
-                         int n_rows, int n_cols, hipStream_t s);
+                         int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s);
+size_t swamp_gemm_i8_scratch_bytes(uint32_t dtype, int m, int n_rows, int n_cols);
+int swamp_launch_split_reduce(const float *d_part, float *d_y, int pieces, size_t n,
+                              hipStream_t s);
 int swamp_launch_rmsnorm_rows(const float *d_x, const float *d_norm_w, float eps, void *d_out,
                               uint32_t out_type, int n_tok, int n_cols, hipStream_t s);
 int swamp_launch_swiglu(const float *d_gate, const float *d_up, void *d_out, uint32_t out_type,

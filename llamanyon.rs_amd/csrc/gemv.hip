@@ -192,6 +192,7 @@ int launch_one(uint32_t dtype, const void *d_w, const float *d_x, float *d_y, in
   float *ys[1] = {d_y};
   const int tr = tile_rows_for(dtype, n_cols, n_rows, kX32);
   build_matset(ms, 1, ws, ys, &n_rows, tr);
+  ms.wpc = waves_per_cu_for(dtype, n_cols, n_rows, kX32);
   return dispatch<kProNone, kX32>(dtype, ms, d_x, Pro{}, n_cols, tr, s);
 }
 

@@ -551,6 +551,7 @@ struct MatSet {
   int rows[kMaxMats];
   int tile_end[kMaxMats];  // cumulative tile counts
   int n;
+  int wpc;  // waves per CU the persistent grid aims for (launch_items)
 };
 
 struct TileRef {
@@ -855,8 +856,8 @@ bool item_path_ok(uint32_t dt, int n_cols) {
 // Launch shape: waves per CU the persistent grid aims for, and rows per
 // tile (SWAMP_GEMV_WAVES_PER_CU / SWAMP_GEMV_ROWS override them).
 struct Tuning {
-  int waves_per_cu = 4;
-  int rows = 0;  // 0: chosen per shape
+  int waves_per_cu = 0;  // 0: chosen per shape
+  int rows = 0;          // 0: chosen per shape
   Tuning() {
     if (const char *s = std::getenv("SWAMP_GEMV_WAVES_PER_CU")) {
       int v = std::atoi(s);
@@ -879,7 +880,7 @@ int launch_items(const MatSet &ms, const float *x, const Pro &pro, int n_cols, h
   if (ipr > kPPT * 64 * kWaves) return SWAMP_ESHAPE;
   const int n_tiles = ms.tile_end[ms.n - 1];
   const int cus = swamp::device_info().num_cus;
-  int grid = cus * std::max(1, tuning().waves_per_cu / kWaves);
+  int grid = cus * std::max(1, ms.wpc / kWaves);
   if (grid > n_tiles) grid = n_tiles;
   if (grid < 1) return SWAMP_OK;
   if (ms.n == 1)
@@ -896,6 +897,7 @@ int launch_items(const MatSet &ms, const float *x, const Pro &pro, int n_cols, h
 int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, const int *rows,
                  int tile_rows) {
   ms.n = n;
+  ms.wpc = 4;
   int acc = 0;
   for (int i = 0; i < n; i++) {
     ms.w[i] = static_cast<const uint8_t *>(ws[i]);
@@ -910,9 +912,23 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
 // Waves per workgroup for a row of ipr items (matches launch_rows).
 int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
 
+// Waves per CU of the persistent grid: 4 (one per SIMD); 8 for the fp32-x
+// Q4_0 / Q4_K kernels on large matrices (at least 16384 rows, or rows of
+// more than 4096 weights), whose heavier arithmetic per weight needs a
+// second wave per SIMD to keep loads in flight (measured sweep, 8B
+// shapes: gate+up 17.0 -> 15.5 us, down 10.6 -> 9.8 us, Q4_K lm_head
+// 64.4 -> 60.3 us).
+int waves_per_cu_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
+  if (tuning().waves_per_cu) return tuning().waves_per_cu;
+  if (x32 && (dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && (total_rows >= 16384 || n_cols > 4096))
+    return 8;
+  return 4;
+}
+
 // Rows per tile: 4 when every workgroup of the grid gets at least 8 tiles,
 // else 2 when it gets at least 2, else 1; always 1 when a lane holds
-// several items (rows of more than 512 items); Q6_K capped lower.  Longer tile runs per wave
+// several items (rows of more than 512 items); Q6_K capped lower; at most
+// 2 with 8 waves per CU.  Longer tile runs per wave
 // hide the first tile's latency and the x prologue; shorter tiles keep
 // small matrices spread over the whole chip.
 int tile_rows_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
@@ -923,9 +939,11 @@ int tile_rows_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   if (dt == SWAMP_Q6_K) cap = ipr <= 256 ? 2 : 1;
   // Q8_0 with fp32 x: the register budget allows 2 rows
   if (dt == SWAMP_Q8_0 && x32) cap = std::min(cap, 2);
+  const int wpc = waves_per_cu_for(dt, n_cols, total_rows, x32);
+  if (wpc >= 8) cap = std::min(cap, 2);
   if (tuning().rows) return std::min(tuning().rows, cap);
   const int cus = swamp::device_info().num_cus;
-  const long slots = long(cus) * std::max(1, tuning().waves_per_cu / waves_for(ipr));
+  const long slots = long(cus) * std::max(1, wpc / waves_for(ipr));
   int r = 1;
   if (long(total_rows) / 4 >= 8 * slots) r = 4;
   else if (long(total_rows) / 2 >= 2 * slots) r = 2;
@@ -1019,6 +1037,7 @@ int launch_multi(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
     MatSet ms;
     const int tr = tile_rows_for(dt, n_cols, total, kX32);
     build_matset(ms, n, ws, ys, rows, tr);
+    ms.wpc = waves_per_cu_for(dt, n_cols, total, kX32);
     int rc = dispatch<kPro, kX32>(dt, ms, d_x, pro, n_cols, tr, s);
     if (rc) return rc;
   }

@@ -34,6 +34,7 @@ int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w, const float *d_gat
   float *ys[1] = {d_y};
   const int tr = tile_rows_for(dtype, n_cols, n_rows, true);
   build_matset(ms, 1, ws, ys, &n_rows, tr);
+  ms.wpc = waves_per_cu_for(dtype, n_cols, n_rows, true);
   Pro pro;
   pro.x2 = d_up;
   if (accumulate) return dispatch<kProSwiGLUAcc, true>(dtype, ms, d_gate, pro, n_cols, tr, s);

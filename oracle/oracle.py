@@ -31,7 +31,41 @@ def lib() -> ctypes.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         build()
-    L = ctypes.CDLL(LIB_PATH)
+    _lib = _bind(ctypes.CDLL(LIB_PATH))
+    return _lib
+
+
+# Flags of the CPU-baseline build: optimised for the host it runs on, with
+# no contraction and no fast-math, so the arithmetic stays the reference's
+# (Rust never contracts a*b+c) and only the speed differs from liboracle.so.
+NATIVE_FLAGS = ["-O3", "-march=native", "-std=c11", "-fPIC", "-shared", "-pthread",
+                "-ffp-contract=off", "-fno-fast-math"]
+
+
+def use_native_build() -> str:
+    """Switch this module to a build of swamp_oracle.c made now, on this host,
+    with NATIVE_FLAGS (bench.py's cpu_baseline: -march=native must be compiled
+    on the CPU that runs it).  Returns a description of the build in use;
+    keeps liboracle.so when no C compiler is found or the build fails."""
+    global _lib
+    import shutil
+    import tempfile
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        lib()
+        return "oracle/liboracle.so (-O2; no C compiler for a native build)"
+    out = os.path.join(tempfile.mkdtemp(prefix="swamp_oracle_native_"), "liboracle_native.so")
+    cmd = [cc] + NATIVE_FLAGS + ["-o", out, os.path.join(ORACLE_DIR, "swamp_oracle.c"), "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        lib()
+        return "oracle/liboracle.so (-O2; native build failed: " + r.stderr.strip()[-200:] + ")"
+    _lib = _bind(ctypes.CDLL(out))
+    return os.path.basename(cc) + " " + " ".join(f for f in NATIVE_FLAGS if f not in
+                                                  ("-fPIC", "-shared", "-pthread"))
+
+
+def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     u32, i32, f32 = ctypes.c_uint32, ctypes.c_int, ctypes.c_float
     sig = {
         "or_block_size": (c_size, [u32]),
@@ -63,7 +97,6 @@ def lib() -> ctypes.CDLL:
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = L
     return L
 
 

@@ -453,12 +453,16 @@ int or_fused_gemv_q6k(const uint8_t *w_raw, size_t w_len, const float *x,
 /* ---------------------------------------------------------------------- */
 
 typedef struct {
-  int kind; /* 0 = Q4_K fused, 1 = dense f32 dot over deq, 2 = Q6_K fused */
+  int kind; /* 0 = Q4_K fused, 1 = dense f32 dot over deq, 2 = Q6_K fused,
+               3 = Q4_K batched (bs tokens) */
   const uint8_t *raw;
   const float *deq;
   const float *x;
   float *out;
   size_t nc, rs, re;
+  const float *const *xp; /* kind 3: token inputs */
+  float *const *op;       /* kind 3: token outputs (whole rows) */
+  size_t bs;
 } slice_job;
 
 static void run_slice(const slice_job *j) {
@@ -470,6 +474,14 @@ static void run_slice(const slice_job *j) {
   } else if (j->kind == 2) {
     size_t nb = j->nc / 256;
     q6k_scalar(j->raw + j->rs * nb * 210, j->x, j->out + j->rs, rc, nb);
+  } else if (j->kind == 3) {
+    /* linear.rs:215-233: the slice's rows of every token output */
+    size_t nb = j->nc / 256;
+    float **op = (float **)malloc(j->bs * sizeof(float *));
+    if (!op) return;
+    for (size_t t = 0; t < j->bs; t++) op[t] = j->op[t] + j->rs;
+    or_fused_gemv_q4k_batched(j->raw + j->rs * nb * 144, j->xp, op, rc, j->nc, j->bs);
+    free(op);
   } else {
     /* linear.rs:81-85: s += deq[i*nc+j] * x[j], sequential f32 */
     for (size_t i = 0; i < rc; i++) {
@@ -564,10 +576,10 @@ int or_forward_linear_batch(uint32_t dtype, const uint8_t *raw, size_t raw_len,
     if (nc % 256 != 0) return -1;
     if (raw_len < or_nbytes_for(12, nr * nc)) return -1;
     memset(outs, 0, bs * nr * sizeof(float)); /* :205-207 */
-    /* :209-236: rows partitioned over threads; inside a slice the batched
-     * scalar kernel runs block -> row -> token.  Each (row, token) value
-     * is a sum of per-block partials added in block order, independent of
-     * the partition, so one call over all rows gives the same bits. */
+    /* :209-236: rows partitioned over n_threads threads (rpt = ceil(nr /
+     * nt)); inside a slice the batched scalar kernel runs block -> row ->
+     * token.  Each (row, token) value is a sum of per-block partials added
+     * in block order, so the result does not depend on the partition. */
     const float **xp = (const float **)malloc(bs * sizeof(float *));
     float **op = (float **)malloc(bs * sizeof(float *));
     if (!xp || !op) {
@@ -578,8 +590,15 @@ int or_forward_linear_batch(uint32_t dtype, const uint8_t *raw, size_t raw_len,
       xp[t] = xs + t * nc;
       op[t] = outs + t * nr;
     }
-    (void)n_threads;
-    int rc = or_fused_gemv_q4k_batched(raw, xp, op, nr, nc, bs);
+    slice_job proto;
+    memset(&proto, 0, sizeof proto);
+    proto.kind = 3;
+    proto.raw = raw;
+    proto.nc = nc;
+    proto.xp = xp;
+    proto.op = op;
+    proto.bs = bs;
+    int rc = run_partitioned(proto, nr, n_threads);
     free(xp); free(op);
     return rc;
   }

@@ -215,6 +215,24 @@ SWAMP_API size_t swamp_qgemm_workspace(uint32_t dtype, uint32_t x_type, int m, i
                                        int n_cols);
 SWAMP_API int swamp_workspace_reserve(void *stream, size_t bytes);
 
+/* swamp_qgemv_batched with every argument, result and error as there, but
+ * allocating nothing: no hipMalloc / hipMallocAsync / hipFree and no
+ * allocating library routine, on any path.  No counterpart in the
+ * reference; it is for callers that cannot allocate (code under graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Its
+ * scratch is a fixed array of SWAMP_NOALLOC_SCRATCH_BYTES (32 MiB) in
+ * device memory that each GPU the library runs on holds until the process
+ * ends; a call whose scratch exceeds it (swamp_qgemv_batched_workspace)
+ * returns SWAMP_EWORKSPACE before launching anything.  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (on two
+ * streams, or from two host threads) race on it and must be ordered by the
+ * caller. */
+#define SWAMP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+SWAMP_API int swamp_qgemv_batched_noalloc(uint32_t dtype, const void *d_w, size_t w_len,
+                                          const float *d_x, float *d_y, int n_tok,
+                                          int n_rows, int n_cols, int accumulate,
+                                          void *stream);
+
 /* Activation producers for the small batch (out_type SWAMP_F32) and the
  * prefill GEMM (SWAMP_BF16: its bf16 x, rounded to nearest even), over
  * n_tok tokens in one pass.

@@ -42,6 +42,7 @@ GPU_SYMBOLS = (
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
     "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
     "swamp_qgemv_batched_workspace", "swamp_qgemm_workspace", "swamp_workspace_reserve",
+    "swamp_qgemv_batched_noalloc",
 )
 # Every symbol include/swamp_gguf.h declares (also in libswamp_gpu.so).
 GGUF_SYMBOLS = (
@@ -123,6 +124,8 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_qgemv_batched_workspace": (c_size, [u32, i32, i32, i32, i32]),
         "swamp_qgemm_workspace": (c_size, [u32, u32, i32, i32, i32]),
         "swamp_workspace_reserve": (i32, [c_vp, c_size]),
+        "swamp_qgemv_batched_noalloc": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, i32, i32,
+                                              c_vp]),
         "swamp_gemv_q8_vnni": (ctypes.c_float, [c_vp, c_vp, i32, ctypes.c_float]),
         # GGUF reader (include/swamp_gguf.h)
         "swamp_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(c_vp)]),
@@ -272,6 +275,15 @@ def qgemv_batched(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_tok: i
                   n_rows: int, n_cols: int, accumulate: bool = False, stream: int = 0) -> None:
     _check(gpu_lib().swamp_qgemv_batched(dtype, d_w, w_len, d_x, d_y, n_tok, n_rows, n_cols,
                                          1 if accumulate else 0, stream), "swamp_qgemv_batched")
+
+
+def qgemv_batched_noalloc(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_tok: int,
+                          n_rows: int, n_cols: int, accumulate: bool = False,
+                          stream: int = 0) -> None:
+    """swamp_qgemv_batched without any allocation (fixed 32 MiB scratch per GPU)."""
+    _check(gpu_lib().swamp_qgemv_batched_noalloc(dtype, d_w, w_len, d_x, d_y, n_tok, n_rows,
+                                                 n_cols, 1 if accumulate else 0, stream),
+           "swamp_qgemv_batched_noalloc")
 
 
 def qgemm(dtype: int, d_w: int, w_len: int, d_x: int, x_type: int, d_y: int, m: int,

@@ -16,10 +16,19 @@
 
 namespace swamp {
 
+// Scratch of swamp_qgemv_batched_noalloc: a fixed array in device memory,
+// one copy per device the library runs on (held until the process ends),
+// shared by every call of that entry point on that device.  Host code uses
+// it only through the address hipGetSymbolAddress returns for the device
+// (g_scratch), never through its name.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 constexpr int kMaxDevices = 64;
 DeviceInfo g_info[kMaxDevices];
 std::once_flag g_once[kMaxDevices];
+void *g_scratch[kMaxDevices];  // device address of `scratch` per device (nullptr: lookup failed)
 
 size_t block_size(uint32_t dt) {
   switch (dt) {
@@ -72,6 +81,14 @@ int ensure_device(int *dev_out) {
         cus > 0)
       g_info[dev].num_cus = cus;
     g_info[dev].device = dev;
+    // this device's copy of the no-alloc scratch array (dev is current)
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) {
+      g_scratch[dev] = p;
+    } else {
+      (void)hipGetLastError();
+      g_scratch[dev] = nullptr;
+    }
   });
   if (dev_out) *dev_out = dev;
   return SWAMP_OK;
@@ -344,6 +361,32 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (n_cols == 0) return fill_zero(d_y, size_t(m) * size_t(n_rows), s);
   Scratch sc = stream_scratch(s, swamp_gemm_scratch_bytes(dtype, x_type, m, n_rows, n_cols));
   return swamp_launch_gemm(dtype, d_w, d_x, x_type, d_y, m, n_rows, n_cols, sc, s);
+}
+
+int swamp_qgemv_batched_noalloc(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x,
+                                float *d_y, int n_tok, int n_rows, int n_cols, int accumulate,
+                                void *stream) {
+  if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
+  if (n_tok < 0) return SWAMP_EINVAL;
+  if (dtype == SWAMP_Q6_K && accumulate) return SWAMP_EDTYPE;
+  if (n_tok == 0 || n_rows == 0) return SWAMP_OK;
+  if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
+  if (dtype != SWAMP_Q4_K && n_cols % 64 != 0) return SWAMP_ESHAPE;
+  int dev = 0;
+  if (int rc = ensure_device(&dev)) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_cols == 0)
+    return accumulate ? SWAMP_OK : fill_zero(d_y, size_t(n_tok) * size_t(n_rows), s);
+  const int acc = accumulate ? 1 : 0;
+  const size_t need = swamp_batched_scratch_bytes(dtype, n_tok, n_rows, n_cols, acc);
+  if (need > kNoAllocScratchBytes) return SWAMP_EWORKSPACE;
+  Scratch sc;
+  if (need) {
+    if (!g_scratch[dev]) return SWAMP_EWORKSPACE;
+    sc.base = static_cast<uint8_t *>(g_scratch[dev]);
+    sc.cap = kNoAllocScratchBytes;
+  }
+  return swamp_launch_gemv_batched(dtype, d_w, d_x, d_y, n_tok, n_rows, n_cols, acc, sc, s);
 }
 
 size_t swamp_qgemv_batched_workspace(uint32_t dtype, int n_tok, int n_rows, int n_cols,

@@ -19,7 +19,8 @@ Also reported (outside the timed steps):
     launches in a second run of the K steps (events between kernels slow
     the step, so the first run, which gives `value`, has none);
   * per-matrix GB/s (each matrix timed alone, outside the timed region);
-  * the Q4_0 prefill GEMM at 2048 and 512 tokens on the matrix cores, with bf16
+  * the Q4_0 prefill GEMM at 2048 and 512 tokens (mean of 20 back-to-back
+    calls after 10 untimed ones), with bf16
     activations (fraction of the 2.5 PFLOP/s dense bf16 peak) and with
     Q8_0-quantized activations on the int8 MFMA (quantizer included;
     fraction of the 5.0 POP/s dense int8 peak);
@@ -645,9 +646,11 @@ def main():
 
                 for xname, g, peak in (("bf16", g_bf16, BF16_PEAK_TFLOPS),
                                        ("q8_0 (int8 MFMA)", g_int8, INT8_PEAK_TOPS)):
-                    for _ in range(3):
+                    # 10 untimed calls bring the shader clock to its sustained
+                    # level under this load, then the mean of 20 back-to-back
+                    for _ in range(10):
                         g()
-                    reps = 10
+                    reps = 20
                     e0, e1 = (torch.cuda.Event(enable_timing=True),
                               torch.cuda.Event(enable_timing=True))
                     e0.record(stream)

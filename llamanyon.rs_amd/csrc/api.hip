@@ -378,7 +378,8 @@ int swamp_qgemv_batched_noalloc(uint32_t dtype, const void *d_w, size_t w_len, c
   if (n_cols == 0)
     return accumulate ? SWAMP_OK : fill_zero(d_y, size_t(n_tok) * size_t(n_rows), s);
   const int acc = accumulate ? 1 : 0;
-  const size_t need = swamp_batched_scratch_bytes(dtype, n_tok, n_rows, n_cols, acc);
+  const size_t need =
+      swamp_batched_scratch_bytes(dtype, n_tok, n_rows, n_cols, acc, kNoAllocScratchBytes);
   if (need > kNoAllocScratchBytes) return SWAMP_EWORKSPACE;
   Scratch sc;
   if (need) {

@@ -693,10 +693,15 @@ int swamp_launch_split_reduce(const float *d_part, float *d_y, int pieces, size_
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
 
-size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols) {
+size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols,
+                                size_t limit) {
   if (m <= 0 || n_rows <= 0 || n_cols <= 0) return 0;
   if (x_type == SWAMP_Q8_0) return swamp_gemm_i8_scratch_bytes(dtype, m, n_rows, n_cols);
   if (x_type != SWAMP_BF16 || n_cols % kBK != 0) return 0;
+  if (swamp_gemm_dq_route(dtype, m, n_rows, n_cols)) {
+    const size_t dq = swamp_gemm_dq_scratch_bytes(n_rows, n_cols);
+    if (dq <= limit) return dq;
+  }
   switch (dtype) {
     case SWAMP_Q4_0: return plan_bf16<SWAMP_Q4_0>(m, n_rows, n_cols).part_bytes;
     case SWAMP_Q8_0: return plan_bf16<SWAMP_Q8_0>(m, n_rows, n_cols).part_bytes;
@@ -715,6 +720,15 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   if (n_cols % kBK != 0) return SWAMP_ESHAPE;
   // activation offsets are 32-bit (buffer descriptors)
   if (size_t(m) * size_t(n_cols) * 2 > size_t(UINT32_MAX)) return SWAMP_ESHAPE;
+  // long prompts: dequantize once to bf16 and run a plain bf16 GEMM, when
+  // the scratch for it is there (else the fused kernel below)
+  if (swamp_gemm_dq_route(dtype, m, n_rows, n_cols) &&
+      sc.cap - sc.used >= swamp_gemm_dq_scratch_bytes(n_rows, n_cols)) {
+    const size_t used = sc.used;
+    const int rc = swamp_launch_gemm_dq(dtype, d_w, d_x, d_y, m, n_rows, n_cols, sc, s);
+    if (rc != kDqUnavailable) return rc;
+    sc.used = used;
+  }
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint16_t *x = static_cast<const uint16_t *>(d_x);
   switch (dtype) {

@@ -1,0 +1,169 @@
+// gemm_dq.hip -- the prefill GEMM's dequantize-once route, for prompts long
+// enough to amortise it: the weight rows are dequantized to bf16 in row
+// chunks (dequant.hip, each value the reference's exact fp32 weight rounded
+// to nearest even -- the same bf16 values the fused kernel of gemm.hip
+// feeds its matrix cores), and each chunk is multiplied by the bf16
+// activations with hipBLASLt (a plain bf16 x bf16 -> fp32 GEMM, fp32
+// accumulation) into its column block of y.
+//
+// Layout for the library (column-major): y row-major [m][n_rows] is the
+// column-major n_rows x m matrix D with ld n_rows; a chunk of weight rows
+// [r0, r1) is the column-major K x (r1 - r0) matrix A with ld K, used
+// transposed; x row-major [m][K] is the column-major K x m matrix B with ld
+// K.  D[r0:r1, :] = A^T B, written at y + r0 with ld n_rows.
+#include <hipblaslt/hipblaslt.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "swamp_common.hpp"
+
+namespace {
+
+constexpr size_t kChunkTarget = size_t(128) << 20;  // bf16 bytes of weights per chunk
+constexpr size_t kLtWorkspace = size_t(32) << 20;   // hipBLASLt workspace offered
+
+struct LtPlan {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t ws = 0;
+  bool ok = false;
+};
+
+struct LtState {
+  std::mutex mu;
+  hipblasLtHandle_t handle = nullptr;
+  bool init = false, ok = false;
+  std::map<std::tuple<int, int, int, int>, LtPlan> plans;  // (m, rows, K, ld)
+};
+
+LtState &lt_state(int dev) {
+  static LtState st[64];
+  return st[dev & 63];
+}
+
+// Rows per chunk: whole 256-row tiles, at most about kChunkTarget bytes of
+// bf16.  (Chunks dequantized on a second stream beside the previous chunk's
+// GEMM measured slower: two smaller GEMMs lose more than the overlap wins.)
+int chunk_rows(int n_rows, int n_cols) {
+  const size_t total = size_t(n_rows) * size_t(n_cols) * 2;
+  const int chunks = int(std::max<size_t>(1, (total + kChunkTarget - 1) / kChunkTarget));
+  int r = (n_rows + chunks - 1) / chunks;
+  r = (r + 255) / 256 * 256;
+  return std::min(r, n_rows);
+}
+
+
+// The matmul plan for one chunk shape (created once, kept for the process).
+const LtPlan *lt_plan(int dev, int m, int rows, int k, int ld) {
+  LtState &st = lt_state(dev);
+  std::lock_guard<std::mutex> lock(st.mu);
+  if (!st.init) {
+    st.init = true;
+    st.ok = hipblasLtCreate(&st.handle) == HIPBLAS_STATUS_SUCCESS;
+  }
+  if (!st.ok) return nullptr;
+  auto key = std::make_tuple(m, rows, k, ld);
+  auto it = st.plans.find(key);
+  if (it != st.plans.end()) return it->second.ok ? &it->second : nullptr;
+  LtPlan &p = st.plans[key];
+  bool ok = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
+            HIPBLAS_STATUS_SUCCESS;
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta,
+                                             sizeof(ta)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb,
+                                             sizeof(tb)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, uint64_t(k), uint64_t(rows),
+                                         int64_t(k)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, uint64_t(k), uint64_t(m),
+                                         int64_t(k)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.d, HIP_R_32F, uint64_t(rows), uint64_t(m),
+                                         int64_t(ld)) == HIPBLAS_STATUS_SUCCESS;
+  if (ok) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    const uint64_t cap = kLtWorkspace;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(
+                   pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof(cap)) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int n = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(st.handle, p.op, p.a, p.b, p.d, p.d, pref, 1, res,
+                                               &n) == HIPBLAS_STATUS_SUCCESS &&
+         n >= 1 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= cap;
+    if (ok) {
+      p.algo = res[0].algo;
+      p.ws = res[0].workspaceSize;
+    }
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  }
+  p.ok = ok;
+  return ok ? &p : nullptr;
+}
+
+int route_forced() {  // tuning override: SWAMP_GEMM_ROUTE=fused|dq
+  static const int v = [] {
+    const char *e = std::getenv("SWAMP_GEMM_ROUTE");
+    if (!e) return 0;
+    if (e[0] == 'f') return 1;
+    if (e[0] == 'd') return 2;
+    return 0;
+  }();
+  return v;
+}
+
+}  // namespace
+
+bool swamp_gemm_dq_route(uint32_t dtype, int m, int n_rows, int n_cols) {
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return false;
+  if (route_forced()) return route_forced() == 2;
+  // The dequant pass costs about 2.6 bytes of HBM traffic per weight (read
+  // the blocks, write bf16): it pays once every weight meets enough tokens.
+  // Measured (8B Q4_0 shapes, fused / this route, us): 1024 tokens gate_up
+  // 249-271 / 281-307, down 140-147 / 160-174; 2048 tokens gate_up 481 /
+  // 493, down 268 / 261, qkv 119 / 112; 4096 tokens gate_up 877 / 857,
+  // down 439 / 407, qkv 226 / 201; 70B at 4096 tokens o_proj 583 / 506,
+  // gate_up 3507 / 3204.
+  return m >= 2048 && n_rows >= 1024 && n_cols >= 1024;
+}
+
+size_t swamp_gemm_dq_scratch_bytes(int n_rows, int n_cols) {
+  const size_t w = size_t(chunk_rows(n_rows, n_cols)) * size_t(n_cols) * 2;
+  return ((w + 255) & ~size_t(255)) + kLtWorkspace;
+}
+
+int swamp_launch_gemm_dq(uint32_t dtype, const void *d_w, const void *d_x, float *d_y, int m,
+                         int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return SWAMP_ENODEVICE;
+  const int cr = chunk_rows(n_rows, n_cols);
+  // every chunk's plan (at most two shapes) before anything is launched: a
+  // shape the library has no algorithm for leaves the call to the fused
+  // kernel
+  const int last = n_rows - (n_rows - 1) / cr * cr;
+  const LtPlan *p_full = lt_plan(dev, m, cr, n_cols, n_rows);
+  const LtPlan *p_last = last == cr ? p_full : lt_plan(dev, m, last, n_cols, n_rows);
+  if (!p_full || !p_last) return kDqUnavailable;
+  void *wb = sc.get(size_t(cr) * size_t(n_cols) * 2);
+  void *ws = sc.get(kLtWorkspace);
+  if (!wb || !ws) return kDqUnavailable;
+  const size_t rb = swamp::row_bytes(int(dtype), size_t(n_cols));
+  const float alpha = 1.0f, beta = 0.0f;
+  for (int r0 = 0; r0 < n_rows; r0 += cr) {
+    const int rows = std::min(cr, n_rows - r0);
+    const LtPlan *p = rows == cr ? p_full : p_last;
+    const uint8_t *w = static_cast<const uint8_t *>(d_w) + size_t(r0) * rb;
+    if (int rc = swamp_launch_dequant_bf16(dtype, w, wb, size_t(rows) * size_t(n_cols), s))
+      return rc;
+    float *y = d_y + r0;
+    if (hipblasLtMatmul(lt_state(dev).handle, p->op, &alpha, wb, p->a, d_x, p->b, &beta, y, p->d,
+                        y, p->d, &p->algo, ws, p->ws, s) != HIPBLAS_STATUS_SUCCESS)
+      return SWAMP_ELAUNCH;
+  }
+  return SWAMP_OK;
+}

@@ -679,12 +679,13 @@ size_t kgroup_bytes(int n_tok, int n_rows, int n_cols, int accumulate) {
 }  // namespace
 
 size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols,
-                                   int accumulate) {
+                                   int accumulate, size_t limit) {
   if (n_tok <= 0 || n_rows <= 0 || n_cols <= 0) return 0;
   if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return 0;
   if (gemm_route(n_tok, n_cols, accumulate)) {
     const size_t xb = (size_t(n_tok) * size_t(n_cols) * 2 + 255) & ~size_t(255);
-    return xb + swamp_gemm_scratch_bytes(dtype, SWAMP_BF16, n_tok, n_rows, n_cols);
+    return xb + swamp_gemm_scratch_bytes(dtype, SWAMP_BF16, n_tok, n_rows, n_cols,
+                                         limit > xb ? limit - xb : 0);
   }
   return kgroup_bytes(n_tok, n_rows, n_cols, accumulate);
 }

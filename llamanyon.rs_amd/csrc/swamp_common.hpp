@@ -144,6 +144,8 @@ inline Scratch stream_scratch(hipStream_t s, size_t bytes) {
 // assume the arguments have been validated by api.cpp.
 int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
                          size_t n, hipStream_t s);
+int swamp_launch_dequant_bf16(uint32_t dtype, const void *d_raw, void *d_dst, size_t n,
+                              hipStream_t s);
 int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x,
                       float *d_y, int n_rows, int n_cols, hipStream_t s);
 int swamp_launch_gemv_f16x(uint32_t dtype, const void *d_w, const float *d_x,
@@ -163,8 +165,19 @@ int swamp_launch_gemv_swiglu(uint32_t dtype, const void *d_w,
 // Scratch bytes a call will take from its region (0: none), from the same
 // plans the launchers follow.
 size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols,
-                                   int accumulate);
-size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols);
+                                   int accumulate, size_t limit = SIZE_MAX);
+// limit: scratch the caller can offer; a route that needs more is not taken.
+size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols,
+                                size_t limit = SIZE_MAX);
+// The bf16 GEMM's dequantize-once route (gemm_dq.hip): whether a shape takes
+// it, its scratch, and the launcher, which returns kDqUnavailable, having
+// launched nothing, when the scratch or a library plan for the shape is
+// missing (the caller then runs the fused kernel).
+constexpr int kDqUnavailable = 1;
+bool swamp_gemm_dq_route(uint32_t dtype, int m, int n_rows, int n_cols);
+size_t swamp_gemm_dq_scratch_bytes(int n_rows, int n_cols);
+int swamp_launch_gemm_dq(uint32_t dtype, const void *d_w, const void *d_x, float *d_y, int m,
+                         int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s);
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,
                               const float *d_x, float *d_y, int n_tok,
                               int n_rows, int n_cols, int accumulate,

@@ -55,8 +55,10 @@ def test_workspace_queries(pkg, torch_dev):
     # few tiles: K split into pieces -> scratch
     assert L.swamp_qgemm_workspace(Q4_0, BF16, 64, 512, 4096) > 0
     assert L.swamp_qgemm_workspace(Q4_0, Q8_0, 64, 512, 4096) > 0
-    # a full round of tiles: no split
-    assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 28672, 4096) == 0
+    # a full round of tiles on the fused kernel: no split
+    assert L.swamp_qgemm_workspace(Q4_0, BF16, 512, 28672, 4096) == 0
+    # a long prompt: dequantize-once route (bf16 weight chunk + library workspace)
+    assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 28672, 4096) > 0
     # small batch: K groups on a short matrix; more than 16 tokens: bf16 x
     assert L.swamp_qgemv_batched_workspace(Q4_K, 16, 4096, 14336, 0) > 0
     assert L.swamp_qgemv_batched_workspace(Q4_0, 40, 4096, 4096, 0) >= 40 * 4096 * 2

@@ -424,9 +424,10 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also print one line per extra workload (8B small-batch Q4_K sweep, "
                          "70B decode and prefill) after the main line")
-    ap.add_argument("--pmc-gemm", action="store_true",
-                    help="only run 5 calls of the 2048-token gate+up prefill GEMM (Q4_0 x bf16) "
-                         "and one 256 MiB device copy (for rocprofv3 --pmc), no JSON")
+    ap.add_argument("--pmc-gemm", nargs="?", const="bf16", choices=["bf16", "int8"],
+                    help="only run 5 calls of the 2048-token gate+up prefill GEMM (Q4_0 weights; "
+                         "x bf16, or int8: x quantized to Q8_0 on the device, then the int8 "
+                         "GEMM) and one 256 MiB device copy (for rocprofv3 --pmc), no JSON")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
@@ -472,12 +473,22 @@ def main():
         pm = PREFILL_MS[0]
         raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x100, 0.02, rows, k)
         w = torch.from_numpy(raw).cuda()
-        xg = torch.from_numpy(pkg.to_bf16_bits(pkg.fill_normal(SEED ^ 0x200, 1.0, pm, k))
-                              .view(np.int16)).cuda()
+        xf = pkg.fill_normal(SEED ^ 0x200, 1.0, pm, k)
         yg = torch.empty((pm, rows), dtype=torch.float32, device="cuda")
+        if args.pmc_gemm == "int8":
+            xd = torch.from_numpy(xf).cuda()
+            xg = torch.empty(pm * k // 32 * 34, dtype=torch.uint8, device="cuda")
+        else:
+            xg = torch.from_numpy(pkg.to_bf16_bits(xf).view(np.int16)).cuda()
         for _ in range(5):
-            rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xg.data_ptr(), pkg.BF16,
-                                 yg.data_ptr(), pm, rows, k, s)
+            if args.pmc_gemm == "int8":
+                rc = lib.swamp_quantize_q8_0(xd.data_ptr(), pkg.F32, xg.data_ptr(), pm * k, s)
+                if rc == 0:
+                    rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xg.data_ptr(),
+                                         pkg.Q8_0, yg.data_ptr(), pm, rows, k, s)
+            else:
+                rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xg.data_ptr(), pkg.BF16,
+                                     yg.data_ptr(), pm, rows, k, s)
             if rc != 0:
                 raise pkg.GpuError(rc, "swamp_qgemm")
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -485,7 +496,7 @@ def main():
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
-        print(f"pmc gemm: 5 x swamp_qgemm Q4_0 {name} {pm}x{rows}x{k} (bf16 x), then a "
+        print(f"pmc gemm: 5 x swamp_qgemm Q4_0 {name} {pm}x{rows}x{k} ({args.pmc_gemm} x), then a "
               f"{src.numel()}-byte device copy", flush=True)
         return
 

@@ -122,6 +122,17 @@ SWAMP_API int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes,
                       const int *row_counts, const float *d_x,
                       float *const *d_ys, int n_cols, void *stream);
 
+/* Several GEMVs, each with its own weights, shape, x and y, in one call:
+ * y_i = W_i x_i, each OVERWRITTEN, i < n.  Replaces forward_gemvs
+ * (swamp-engine/src/linear.rs:278-333), which zeroes each output and runs
+ * the specs' row slices in one parallel section.  Arguments per GEMV as
+ * swamp_qgemv (any of its dtypes; the reference sends every non-Q4_K spec
+ * to the Q6_K kernel, here each dtype gets its own); every GEMV is
+ * validated before any is launched; the GEMVs run in order on the stream. */
+SWAMP_API int swamp_qgemv_many(int n, const uint32_t *dtypes, const void *const *d_ws,
+                               const size_t *w_lens, const int *n_rows, const int *n_cols,
+                               const float *const *d_xs, float *const *d_ys, void *stream);
+
 /* RMSNorm fused into the GEMV's x prologue: y_m = W_m x_norm with
  * x_norm = (x * inv_rms) * norm_w, inv_rms = 1 / sqrt(sum(x^2) / n_cols +
  * eps), each y_m OVERWRITTEN; x_norm is not written.  Replaces the
@@ -182,10 +193,17 @@ SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     32-weight block) against W's int8 codes (Q4_0: nibble - 8), each
  *     block's int32 result scaled by d_w * d_x into fp32.  Q4_0 and Q8_0
  *     weights only; n_cols a multiple of 128.
- * dtype Q4_0, Q8_0 or Q4_K (Q4_K with bf16 x only; Q6_K -> SWAMP_EDTYPE);
- * bf16 x needs n_cols a multiple of 64.  When the tiles do not fill the
- * GPU, K is split across workgroups whose partial tiles go to scratch and
- * are summed in piece order by a second kernel (deterministic). */
+ * dtype Q4_0, Q8_0, Q4_K or Q6_K (Q4_K and Q6_K with bf16 x only); bf16 x
+ * needs n_cols a multiple of 64.
+ * Below 2048 tokens (bf16 x) the fused kernel dequantizes weight tiles in
+ * registers to bf16; when the tiles do not fill the GPU, K is split across
+ * workgroups whose partial tiles go to scratch and are summed in piece
+ * order by a second kernel (deterministic).  From 2048 tokens, and for Q6_K
+ * at any length, the weights are dequantized once per call to bf16 in
+ * scratch (row chunks of at most 128 MB; the same bf16 values) and each
+ * chunk is multiplied by a hipBLASLt bf16 GEMM with fp32 accumulation; when
+ * that scratch cannot be had the fused kernel runs (Q6_K:
+ * SWAMP_EWORKSPACE). */
 SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);

@@ -42,7 +42,7 @@ GPU_SYMBOLS = (
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
     "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
     "swamp_qgemv_batched_workspace", "swamp_qgemm_workspace", "swamp_workspace_reserve",
-    "swamp_qgemv_batched_noalloc",
+    "swamp_qgemv_batched_noalloc", "swamp_qgemv_many",
 )
 # Every symbol include/swamp_gguf.h declares (also in libswamp_gpu.so).
 GGUF_SYMBOLS = (
@@ -108,6 +108,10 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_qdequant": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp]),
         "swamp_qgemv": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
         "swamp_qgemv_f16x": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
+        "swamp_qgemv_many": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
+                                   ctypes.POINTER(c_size), ctypes.POINTER(i32),
+                                   ctypes.POINTER(i32), ctypes.POINTER(c_vp),
+                                   ctypes.POINTER(c_vp), c_vp]),
         "swamp_qgemv_multi": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
                                     ctypes.POINTER(c_size), ctypes.POINTER(i32), c_vp,
                                     ctypes.POINTER(c_vp), i32, c_vp]),
@@ -250,6 +254,17 @@ def qgemv_multi(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int
     ys = (c_vp * n)(*d_ys)
     _check(gpu_lib().swamp_qgemv_multi(n, u32s, ws, lens, rows, d_x, ys, n_cols, stream),
            "swamp_qgemv_multi")
+
+
+def qgemv_many(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int],
+               n_rows: Sequence[int], n_cols: Sequence[int], d_xs: Sequence[int],
+               d_ys: Sequence[int], stream: int = 0) -> None:
+    """forward_gemvs: several GEMVs, each with its own x and shape, one call."""
+    n = len(dtypes)
+    _check(gpu_lib().swamp_qgemv_many(n, (ctypes.c_uint32 * n)(*dtypes), (c_vp * n)(*d_ws),
+                                      (c_size * n)(*w_lens), (ctypes.c_int * n)(*n_rows),
+                                      (ctypes.c_int * n)(*n_cols), (c_vp * n)(*d_xs),
+                                      (c_vp * n)(*d_ys), stream), "swamp_qgemv_many")
 
 
 def qgemv_rmsnorm(dtypes: Sequence[int], d_ws: Sequence[int], w_lens: Sequence[int],

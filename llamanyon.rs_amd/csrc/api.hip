@@ -296,6 +296,29 @@ int swamp_qgemv_multi(int n_mats, const uint32_t *dtypes, const void *const *d_w
                                  static_cast<hipStream_t>(stream));
 }
 
+int swamp_qgemv_many(int n, const uint32_t *dtypes, const void *const *d_ws,
+                     const size_t *w_lens, const int *n_rows, const int *n_cols,
+                     const float *const *d_xs, float *const *d_ys, void *stream) {
+  if (n < 0) return SWAMP_EINVAL;
+  if (n == 0) return SWAMP_OK;
+  if (!dtypes || !d_ws || !w_lens || !n_rows || !n_cols || !d_xs || !d_ys) return SWAMP_EINVAL;
+  for (int i = 0; i < n; i++) {  // every GEMV is checked before any is launched
+    if (int rc = check_gemv_args(dtypes[i], d_ws[i], w_lens[i], n_rows[i], n_cols[i])) return rc;
+    if (!d_xs[i] || !d_ys[i] || !aligned(d_xs[i], 16) || !aligned(d_ys[i], 4)) return SWAMP_EINVAL;
+  }
+  if (int rc = ensure_device(nullptr)) return rc;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int i = 0; i < n; i++) {
+    if (n_rows[i] == 0) continue;
+    const int rc = n_cols[i] == 0
+                       ? fill_zero(d_ys[i], size_t(n_rows[i]), s)
+                       : swamp_launch_gemv(dtypes[i], d_ws[i], d_xs[i], d_ys[i], n_rows[i],
+                                           n_cols[i], s);
+    if (rc) return rc;
+  }
+  return SWAMP_OK;
+}
+
 int swamp_qgemv_rmsnorm(int n_mats, const uint32_t *dtypes, const void *const *d_ws,
                         const size_t *w_lens, const int *row_counts, const float *d_x,
                         const float *d_norm_w, float eps, float *const *d_ys, int n_cols,
@@ -351,8 +374,7 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
   if (m < 0) return SWAMP_EINVAL;
   if (x_type != SWAMP_BF16 && x_type != SWAMP_Q8_0) return SWAMP_EDTYPE;
-  if (x_type == SWAMP_Q8_0 && dtype == SWAMP_Q4_K) return SWAMP_EDTYPE;
-  if (dtype == SWAMP_Q6_K) return SWAMP_EDTYPE;
+  if (x_type == SWAMP_Q8_0 && (dtype == SWAMP_Q4_K || dtype == SWAMP_Q6_K)) return SWAMP_EDTYPE;
   if (m == 0 || n_rows == 0) return SWAMP_OK;
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;

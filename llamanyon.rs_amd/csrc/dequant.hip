@@ -252,24 +252,28 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
 // the workgroup's 16 KB are stored as 16-byte pieces of consecutive threads
 // (each store instruction writes 1 KB of consecutive bytes).  dst is the
 // workgroup's first output; `valid` pieces (of 1024) are stored.
+// Piece p = 4t + c sits at lds[c][t] (writes: consecutive lanes, consecutive
+// 16-byte slots); rows are padded by one slot so the reads, lds[p & 3][p >> 2]
+// for p = 256c + t, spread consecutive lanes over four rows without bank
+// conflicts.
+constexpr int kStageRow = 257;
+
 __device__ __forceinline__ void store32_bf16_wg(__bf16 *dst, const float (&v)[32],
-                                                uint4 (*lds)[256], size_t valid) {
+                                                uint4 (*lds)[kStageRow], size_t valid) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     bf16x8_t b;
 #pragma unroll
     for (int j = 0; j < 8; j++) b[j] = __bf16(v[8 * c + j]);
-    // piece 4t + c of the workgroup lives at lds[(4t + c) / 256][(4t + c) % 256]
-    const int piece = 4 * t + c;
-    lds[piece >> 8][piece & 255] = __builtin_bit_cast(uint4, b);
+    lds[c][t] = __builtin_bit_cast(uint4, b);
   }
   __syncthreads();
   uint4 *out = reinterpret_cast<uint4 *>(dst);
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const int piece = 256 * c + t;
-    if (size_t(piece) < valid) out[piece] = lds[c][t];
+    if (size_t(piece) < valid) out[piece] = lds[piece & 3][piece >> 2];
   }
 }
 
@@ -279,7 +283,7 @@ template <int DT>
 __global__ void __launch_bounds__(256) blocks_to_bf16_kernel(const uint8_t *__restrict__ raw,
                                                              __bf16 *__restrict__ dst,
                                                              size_t n_blocks) {
-  __shared__ uint4 lds[4][256];
+  __shared__ uint4 lds[4][kStageRow];
   const size_t b0 = size_t(blockIdx.x) * 256;
   const size_t b = b0 + threadIdx.x;
   const bool live = b < n_blocks;
@@ -323,7 +327,7 @@ __global__ void __launch_bounds__(256) blocks_to_bf16_kernel(const uint8_t *__re
 __global__ void __launch_bounds__(256) q4k_to_bf16_kernel(const uint8_t *__restrict__ raw,
                                                           __bf16 *__restrict__ dst,
                                                           size_t n_sub) {
-  __shared__ uint4 lds[4][256];
+  __shared__ uint4 lds[4][kStageRow];
   const size_t u0 = size_t(blockIdx.x) * 256;
   const size_t u = threadIdx.x + u0 < n_sub ? u0 + threadIdx.x : u0;  // dead: re-read the first
   const size_t b = u >> 3;
@@ -380,6 +384,13 @@ int swamp_launch_dequant_bf16(uint32_t dtype, const void *d_raw, void *d_dst, si
     if (n % 256 != 0) return SWAMP_EINVAL;
     q4k_to_bf16_kernel<<<grid, 256, 0, s>>>(raw, dst, units);
     break;
+  case SWAMP_Q6_K: {
+    // 210-byte blocks, 2-byte aligned: the 8-outputs-per-thread kernel
+    if (n % 256 != 0) return SWAMP_EINVAL;
+    const dim3 grid8(unsigned(((n + 7) / 8 + 255) / 256));
+    dequant_q6_k_kernel<true, __bf16><<<grid8, 256, 0, s>>>(raw, dst, n);
+    break;
+  }
   default:
     return SWAMP_EDTYPE;
   }

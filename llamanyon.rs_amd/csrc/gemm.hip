@@ -700,7 +700,7 @@ size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_ro
   if (x_type != SWAMP_BF16 || n_cols % kBK != 0) return 0;
   if (swamp_gemm_dq_route(dtype, m, n_rows, n_cols)) {
     const size_t dq = swamp_gemm_dq_scratch_bytes(n_rows, n_cols);
-    if (dq <= limit) return dq;
+    if (dq <= limit || dtype == SWAMP_Q6_K) return dq;
   }
   switch (dtype) {
     case SWAMP_Q4_0: return plan_bf16<SWAMP_Q4_0>(m, n_rows, n_cols).part_bytes;
@@ -729,6 +729,7 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
     if (rc != kDqUnavailable) return rc;
     sc.used = used;
   }
+  if (dtype == SWAMP_Q6_K) return SWAMP_EWORKSPACE;  // the route above is its only one
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint16_t *x = static_cast<const uint16_t *>(d_x);
   switch (dtype) {

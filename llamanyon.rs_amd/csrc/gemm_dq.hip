@@ -120,6 +120,7 @@ int route_forced() {  // tuning override: SWAMP_GEMM_ROUTE=fused|dq
 }  // namespace
 
 bool swamp_gemm_dq_route(uint32_t dtype, int m, int n_rows, int n_cols) {
+  if (dtype == SWAMP_Q6_K) return true;  // no fused kernel for Q6_K
   if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return false;
   if (route_forced()) return route_forced() == 2;
   // The dequant pass costs about 2.6 bytes of HBM traffic per weight (read

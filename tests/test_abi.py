@@ -108,12 +108,12 @@ def test_argument_validation_precedes_device(pkg):
     assert L.swamp_qgemm(pkg.Q4_0, fake, 1 << 20, fake, pkg.F16, fake, 4, 4, 64, None) == pkg.EDTYPE
     assert L.swamp_qdequant(13, fake, 1 << 20, fake, 64, None) == pkg.EDTYPE
     # Q6_K: whole 256-blocks, 4-byte aligned rows base, enough bytes; no
-    # accumulating batched form and no GEMM
+    # accumulating batched form and no int8 GEMM
     assert L.swamp_qgemv(pkg.Q6_K, fake, 1 << 20, fake, fake, 4, 300, None) == pkg.ESHAPE
     assert L.swamp_qgemv(pkg.Q6_K, fake, 4 * 420 - 1, fake, fake, 4, 512, None) == pkg.ESHAPE
     assert L.swamp_qgemv(pkg.Q6_K, fake + 2, 1 << 20, fake, fake, 4, 512, None) == pkg.EINVAL
     assert L.swamp_qgemv_batched(pkg.Q6_K, fake, 1 << 20, fake, fake, 2, 4, 512, 1, None) == pkg.EDTYPE
-    assert L.swamp_qgemm(pkg.Q6_K, fake, 1 << 20, fake, pkg.BF16, fake, 4, 4, 512, None) == pkg.EDTYPE
+    assert L.swamp_qgemm(pkg.Q6_K, fake, 1 << 20, fake, pkg.Q8_0, fake, 4, 4, 512, None) == pkg.EDTYPE
     assert L.swamp_qdequant(pkg.Q6_K, fake, 419, fake, 512, None) == pkg.ESHAPE
     # fused prologues: one item per lane (n_cols <= 32768, whole items)
     import ctypes

@@ -583,3 +583,37 @@ def test_gguf_upload_then_gemv(pkg, orc, torch_dev, tmp_path):
             ref = orc.forward_linear(dt, host, x, rows, cols, 8)
             deq = orc.dequantize(dt, host, rows * cols).reshape(rows, cols)
             assert orc.normalized_error(down(d_y), ref, deq, x) <= TOL
+
+
+def test_gemv_many(pkg, orc, torch_dev, errlog):
+    """forward_gemvs (linear.rs:278-333): several GEMVs with their own x and
+    shapes in one call, each written over its y; Q4_K and Q6_K as the
+    reference handles them, plus Q4_0 and Q8_0."""
+    torch = torch_dev
+    spec = [(Q4_K, 3000, 4096), (14, 700, 14336), (Q4_0, 4096, 1024), (Q8_0, 33, 64),
+            (Q4_K, 5, 256)]
+    raws = [weights(pkg, dt, r, c, mid=200 + i) for i, (dt, r, c) in enumerate(spec)]
+    xs = [acts(pkg, 1, c, mid=200 + i)[0] for i, (_, _, c) in enumerate(spec)]
+    d_ws = [up(torch, r) for r in raws]
+    d_xs = [up(torch, x) for x in xs]
+    d_ys = [torch.full((r,), float("nan"), dtype=torch.float32, device="cuda") for _, r, _ in spec]
+    say("gemv many", len(spec))
+    pkg.qgemv_many([dt for dt, _, _ in spec], [t.data_ptr() for t in d_ws],
+                   [r.size for r in raws], [r for _, r, _ in spec], [c for _, _, c in spec],
+                   [t.data_ptr() for t in d_xs], [t.data_ptr() for t in d_ys], stream(torch))
+    torch.cuda.synchronize()
+    for (dt, r, c), raw, x, d_y in zip(spec, raws, xs, d_ys):
+        ref = orc.forward_linear(dt, raw, x, r, c, 8)
+        deq = orc.dequantize(dt, raw, r * c).reshape(r, c)
+        err = errlog(f"gemv many dtype={dt} {r}x{c}", orc.normalized_error(down(d_y), ref, deq, x),
+                     path="gemv")
+        assert err <= 1e-6
+    # a bad spec anywhere: nothing is launched
+    d_y0 = torch.full((spec[0][1],), 7.0, dtype=torch.float32, device="cuda")
+    with pytest.raises(pkg.GpuError):
+        pkg.qgemv_many([Q4_K, Q4_K], [d_ws[0].data_ptr(), d_ws[0].data_ptr()],
+                       [raws[0].size, 10], [spec[0][1], spec[0][1]], [4096, 4096],
+                       [d_xs[0].data_ptr()] * 2, [d_y0.data_ptr(), d_y0.data_ptr()],
+                       stream(torch))
+    torch.cuda.synchronize()
+    assert bool((d_y0 == 7.0).all())

@@ -224,3 +224,46 @@ def test_q6k_gguf_upload_then_gemv(pkg, orc, torch_dev, tmp_path):
               stream(torch))
     torch.cuda.synchronize()
     _check(pkg, orc, raw, x, down(d_y), rows, cols)
+
+
+# ------------------------------------------------------------ prefill GEMM
+
+@pytest.mark.parametrize("m,rows,cols", [(64, 1000, 4096), (300, 4096, 14336), (2048, 2048, 4096),
+                                         (7, 333, 1280)])
+def test_q6k_gemm_bf16(pkg, orc, torch_dev, errlog, m, rows, cols):
+    """Q6_K prefill GEMM (bf16 x): the weights dequantized once to bf16 (the
+    dequantizer's exact values, rounded to nearest even) and multiplied by
+    the library GEMM; against forward_linear's Q6_K arm per token on the
+    bf16-rounded x, within the contract (the Q4_K_M lm_head's prefill)."""
+    torch = torch_dev
+    raw = weights(pkg, Q6_K, rows, cols, mid=m ^ rows)
+    x = acts(pkg, m, cols, mid=m ^ rows)
+    xb = pkg.to_bf16_bits(x)
+    x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
+    say("q6k gemm bf16", m, rows, cols)
+    d_w, d_x = up(torch, raw), up(torch, xb.view(np.int16))
+    d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemm(Q6_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), pkg.BF16, d_y.data_ptr(), m, rows,
+              cols, stream(torch))
+    torch.cuda.synchronize()
+    y = down(d_y)
+    assert np.isfinite(y).all()
+    toks = sorted({0, 1, m // 2, m - 1})
+    ref = orc.forward_linear_batch(Q6_K, raw, x_fed[toks], rows, cols, 8)
+    deq = orc.dequantize(Q6_K, raw, rows * cols).reshape(rows, cols)
+    err = errlog(f"q6k gemm bf16 {m}x{rows}x{cols}", orc.normalized_error(y[toks], ref, deq,
+                                                                          x_fed[toks]),
+                 path="gemm_bf16")
+    assert err <= 4e-4
+
+
+def test_q6k_gemm_int8_refused(pkg, torch_dev):
+    torch = torch_dev
+    raw = weights(pkg, Q6_K, 64, 512)
+    d_w = up(torch, raw)
+    d_q = torch.zeros(8 * 512 // 32 * 34, dtype=torch.uint8, device="cuda")
+    d_y = torch.zeros((8, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(pkg.GpuError) as e:
+        pkg.qgemm(Q6_K, d_w.data_ptr(), raw.size, d_q.data_ptr(), 8, d_y.data_ptr(), 8, 64, 512,
+                  stream(torch))
+    assert e.value.code == pkg.EDTYPE

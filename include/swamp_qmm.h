@@ -79,6 +79,18 @@ SWAMP_API size_t swamp_nbytes_for(uint32_t dtype, size_t n_elems);
 SWAMP_API int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
                    float *d_dst, size_t n, void *stream);
 
+/* No counterpart in the reference: the bf16 form of swamp_qdequant, the
+ * pass the prefill GEMM's dequantize-once route runs before its bf16
+ * library GEMM, exported so that its output can be checked bit for bit and
+ * for callers that feed their own bf16 GEMM.  Writes n bf16 values (raw
+ * bits, uint16) to d_dst: each the swamp_qdequant value rounded to nearest
+ * even (NaN stays NaN).  dtype Q4_0, Q8_0 (n a multiple of 32, d_raw 4-byte
+ * aligned), Q4_K (n a multiple of 256, d_raw 16-byte aligned) or Q6_K (n a
+ * multiple of 256, d_raw 2-byte aligned); d_dst 16-byte aligned.
+ * raw_len < nbytes_for(dtype, n) -> SWAMP_ESHAPE. */
+SWAMP_API int swamp_qdequant_bf16(uint32_t dtype, const void *d_raw, size_t raw_len,
+                                  void *d_dst, size_t n, void *stream);
+
 /* Decode GEMV, y = W x, OVERWRITING y[0..n_rows).
  * Replaces forward_linear (swamp-engine/src/linear.rs:14-90) and the
  * kernels it reaches, fused_gemv_q4k (swamp-kernels/src/fused_gemv_q4k.rs:

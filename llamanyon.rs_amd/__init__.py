@@ -37,7 +37,7 @@ MULTI_MAX = 8
 # Every symbol include/swamp_qmm.h declares.
 GPU_SYMBOLS = (
     "swamp_gpu_init", "swamp_strerror", "swamp_block_size", "swamp_type_size",
-    "swamp_nbytes_for", "swamp_qdequant", "swamp_qgemv", "swamp_qgemv_f16x", "swamp_qgemv_multi",
+    "swamp_nbytes_for", "swamp_qdequant", "swamp_qdequant_bf16", "swamp_qgemv", "swamp_qgemv_f16x", "swamp_qgemv_multi",
     "swamp_qgemv_rmsnorm", "swamp_qgemv_swiglu",
     "swamp_qgemv_batched", "swamp_qgemm", "swamp_rmsnorm_rows", "swamp_swiglu",
     "swamp_quantize_q8_0", "swamp_fused_gemv_q4k", "swamp_gemv_q8_vnni",
@@ -106,6 +106,7 @@ def gpu_lib() -> ctypes.CDLL:
         "swamp_type_size": (c_size, [u32]),
         "swamp_nbytes_for": (c_size, [u32, c_size]),
         "swamp_qdequant": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp]),
+        "swamp_qdequant_bf16": (i32, [u32, c_vp, c_size, c_vp, c_size, c_vp]),
         "swamp_qgemv": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
         "swamp_qgemv_f16x": (i32, [u32, c_vp, c_size, c_vp, c_vp, i32, i32, c_vp]),
         "swamp_qgemv_many": (i32, [i32, ctypes.POINTER(u32), ctypes.POINTER(c_vp),
@@ -229,6 +230,14 @@ def init() -> None:
 
 def qdequant(dtype: int, d_raw: int, raw_len: int, d_dst: int, n: int, stream: int = 0) -> None:
     _check(gpu_lib().swamp_qdequant(dtype, d_raw, raw_len, d_dst, n, stream), "swamp_qdequant")
+
+
+def qdequant_bf16(dtype: int, d_raw: int, raw_len: int, d_dst: int, n: int,
+                  stream: int = 0) -> None:
+    """n bf16 values (uint16 bits) at d_dst: swamp_qdequant's values rounded
+    to nearest even."""
+    _check(gpu_lib().swamp_qdequant_bf16(dtype, d_raw, raw_len, d_dst, n, stream),
+           "swamp_qdequant_bf16")
 
 
 def qgemv(dtype: int, d_w: int, w_len: int, d_x: int, d_y: int, n_rows: int, n_cols: int,

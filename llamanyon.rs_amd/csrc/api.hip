@@ -251,6 +251,19 @@ int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len, float *d_d
   return swamp_launch_dequant(dtype, d_raw, d_dst, n, static_cast<hipStream_t>(stream));
 }
 
+int swamp_qdequant_bf16(uint32_t dtype, const void *d_raw, size_t raw_len, void *d_dst, size_t n,
+                        void *stream) {
+  if (!is_weight_dtype(dtype)) return SWAMP_EDTYPE;
+  if (n == 0) return SWAMP_OK;
+  if (!d_raw || !d_dst) return SWAMP_EINVAL;
+  if (n % swamp_block_size(dtype) != 0) return SWAMP_ESHAPE;
+  if (raw_len < swamp_nbytes_for(dtype, n)) return SWAMP_ESHAPE;
+  const uintptr_t al = dtype == SWAMP_Q6_K ? 2 : weight_align(dtype);
+  if (!aligned(d_raw, al) || !aligned(d_dst, 16)) return SWAMP_EINVAL;
+  if (int rc = ensure_device(nullptr)) return rc;
+  return swamp_launch_dequant_bf16(dtype, d_raw, d_dst, n, static_cast<hipStream_t>(stream));
+}
+
 int swamp_qgemv(uint32_t dtype, const void *d_w, size_t w_len, const float *d_x, float *d_y,
                 int n_rows, int n_cols, void *stream) {
   if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;

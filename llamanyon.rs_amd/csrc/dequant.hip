@@ -252,28 +252,30 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
 // the workgroup's 16 KB are stored as 16-byte pieces of consecutive threads
 // (each store instruction writes 1 KB of consecutive bytes).  dst is the
 // workgroup's first output; `valid` pieces (of 1024) are stored.
-// Piece p = 4t + c sits at lds[c][t] (writes: consecutive lanes, consecutive
-// 16-byte slots); rows are padded by one slot so the reads, lds[p & 3][p >> 2]
-// for p = 256c + t, spread consecutive lanes over four rows without bank
-// conflicts.
-constexpr int kStageRow = 257;
+// Thread t writes pieces p = 4t + c, the store reads p = 256c + t.  Piece p
+// sits in 16-byte slot p ^ h(p), with h's two bits (p3 ^ p5, p4) chosen so
+// that any 8 consecutive lanes (and any 16) of either access hit distinct
+// slots modulo 8 (and 16): no bank conflicts with 32 or 64 four-byte banks.
+__device__ __forceinline__ int stage_slot(int p) {
+  return p ^ (((p >> 3) ^ (p >> 5)) & 1) ^ (p >> 3 & 2);
+}
 
-__device__ __forceinline__ void store32_bf16_wg(__bf16 *dst, const float (&v)[32],
-                                                uint4 (*lds)[kStageRow], size_t valid) {
+__device__ __forceinline__ void store32_bf16_wg(__bf16 *dst, const float (&v)[32], uint4 *lds,
+                                                size_t valid) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     bf16x8_t b;
 #pragma unroll
     for (int j = 0; j < 8; j++) b[j] = __bf16(v[8 * c + j]);
-    lds[c][t] = __builtin_bit_cast(uint4, b);
+    lds[stage_slot(4 * t + c)] = __builtin_bit_cast(uint4, b);
   }
   __syncthreads();
   uint4 *out = reinterpret_cast<uint4 *>(dst);
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     const int piece = 256 * c + t;
-    if (size_t(piece) < valid) out[piece] = lds[piece & 3][piece >> 2];
+    if (size_t(piece) < valid) out[piece] = lds[stage_slot(piece)];
   }
 }
 
@@ -283,7 +285,7 @@ template <int DT>
 __global__ void __launch_bounds__(256) blocks_to_bf16_kernel(const uint8_t *__restrict__ raw,
                                                              __bf16 *__restrict__ dst,
                                                              size_t n_blocks) {
-  __shared__ uint4 lds[4][kStageRow];
+  __shared__ uint4 lds[1024];
   const size_t b0 = size_t(blockIdx.x) * 256;
   const size_t b = b0 + threadIdx.x;
   const bool live = b < n_blocks;
@@ -327,7 +329,7 @@ __global__ void __launch_bounds__(256) blocks_to_bf16_kernel(const uint8_t *__re
 __global__ void __launch_bounds__(256) q4k_to_bf16_kernel(const uint8_t *__restrict__ raw,
                                                           __bf16 *__restrict__ dst,
                                                           size_t n_sub) {
-  __shared__ uint4 lds[4][kStageRow];
+  __shared__ uint4 lds[1024];
   const size_t u0 = size_t(blockIdx.x) * 256;
   const size_t u = threadIdx.x + u0 < n_sub ? u0 + threadIdx.x : u0;  // dead: re-read the first
   const size_t b = u >> 3;

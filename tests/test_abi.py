@@ -134,6 +134,19 @@ def test_argument_validation_precedes_device(pkg):
     assert sw(pkg.Q6_K, 768) == pkg.ESHAPE and sw(pkg.Q4_K, 0) == pkg.ESHAPE
     assert sw(pkg.Q8_0, 4096, up=None) == pkg.EINVAL and sw(pkg.Q8_0, 4096, up=fake + 8) == pkg.EINVAL
     assert L.swamp_qdequant(pkg.Q4_0, fake, 35, fake, 64, None) == pkg.ESHAPE
+    # bf16 dequant: weight dtypes only, whole blocks, aligned buffers
+    dq16 = lambda dt, raw, rl, dst, n: L.swamp_qdequant_bf16(dt, raw, rl, dst, n, None)
+    assert dq16(pkg.F32, fake, 1 << 20, fake, 64) == pkg.EDTYPE
+    assert dq16(13, fake, 1 << 20, fake, 64) == pkg.EDTYPE
+    assert dq16(pkg.Q4_0, fake, 35, fake, 64) == pkg.ESHAPE
+    assert dq16(pkg.Q4_0, fake, 1 << 20, fake, 48) == pkg.ESHAPE
+    assert dq16(pkg.Q4_K, fake, 1 << 20, fake, 288) == pkg.ESHAPE
+    assert dq16(pkg.Q6_K, fake, 419, fake, 512) == pkg.ESHAPE
+    assert dq16(pkg.Q4_0, fake + 2, 1 << 20, fake, 64) == pkg.EINVAL
+    assert dq16(pkg.Q4_K, fake + 4, 1 << 20, fake, 256) == pkg.EINVAL
+    assert dq16(pkg.Q6_K, fake + 1, 1 << 20, fake, 256) == pkg.EINVAL
+    assert dq16(pkg.Q8_0, fake, 1 << 20, fake + 8, 64) == pkg.EINVAL
+    assert dq16(pkg.Q8_0, None, 1 << 20, fake, 64) == pkg.EINVAL
     assert L.swamp_quantize_q8_0(fake, pkg.F32, fake, 33, None) == pkg.ESHAPE
     # activation producers: argument errors return before any device work
     rr = lambda ot, t, c, x=fake, w=fake, o=fake: L.swamp_rmsnorm_rows(x, w, 1e-5, o, ot, t, c,

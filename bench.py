@@ -10,7 +10,9 @@ the weights already resident in HBM.  Algorithmic bytes per matrix =
 rows*K*18/32 (Q4_0 blocks) + K*4 (x) + rows*4 (y).
 
 Several full copies of the weight set (> 2x the 256 MB Infinity Cache in
-total) are rotated step by step so every weight byte comes from HBM.
+total) are rotated step by step so every weight byte comes from HBM.  Before
+the W warm-up steps, untimed steps run for --settle seconds (0.3 by default)
+so the card has reached the clock it holds under sustained load.
 
 Also reported (outside the timed steps):
   * roofline of the dominant kernel (the Q4_0 GEMV on lm_head, 70% of the
@@ -416,6 +418,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed decode steps before the warm-up steps")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-threads", type=str, default="6,max",
                     help="thread counts of the CPU baseline, comma-separated; 'max' is every "
@@ -529,6 +533,20 @@ def main():
         if rc != 0:
             raise pkg.GpuError(rc, "swamp_qgemv")
 
+    def settle(fn=lib.swamp_qgemv):
+        # Untimed steps for args.settle seconds before the warm-up steps: under
+        # sustained load the card takes some milliseconds to reach the clock it
+        # then holds (the first 50 steps after a pause run up to 20% slower).
+        t_end = time.perf_counter() + args.settle
+        it = 0
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                for i in range(len(DECODE_SHAPES)):
+                    launch(it % args.copies, i, fn)
+                it += 1
+            torch.cuda.synchronize()
+
+    settle()
     for it in range(args.warmup):
         for i in range(len(DECODE_SHAPES)):
             launch(it % args.copies, i)
@@ -605,6 +623,7 @@ def main():
 
     # ---- the same step on swamp_qgemv_f16x (x rounded to fp16 inside the
     # kernel): a separately labelled line, not the headline
+    settle(lib.swamp_qgemv_f16x)
     for it in range(args.warmup):
         for i in range(n):
             launch(it % args.copies, i, lib.swamp_qgemv_f16x)

@@ -551,7 +551,8 @@ struct MatSet {
   int rows[kMaxMats];
   int tile_end[kMaxMats];  // cumulative tile counts
   int n;
-  int wpc;  // waves per CU the persistent grid aims for (launch_items)
+  int wpc;   // waves per CU the persistent grid aims for (launch_items)
+  bool sets;  // several row sets per workgroup share x (rows of <= 128 items)
 };
 
 struct TileRef {
@@ -598,12 +599,15 @@ __device__ __forceinline__ int store_row(const TileRef &t, int tid) {
   return min(t.row0 + rr, t.nrows - 1);
 }
 
+// live: the tile is this set's (false: a stand-in tile a row set works
+// through so that every wave of the workgroup meets the same barriers; its
+// result is not stored).
 template <int DT, int kPPT, int kRows, int kWaves, bool kAcc, class XF>
 __device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
                                              const XF (&xf)[kPPT], const TileRef &t,
                                              const int (&item)[kPPT],
                                              float (*red)[kRows], int tid, uint32_t m,
-                                             float out_scale, float y_old) {
+                                             float out_scale, float y_old, bool live) {
   const int lane = tid & 63, wave = tid >> 6;
   float acc[kRows];
 #pragma unroll
@@ -616,14 +620,14 @@ __device__ __forceinline__ void consume_tile(const Raw<DT> (&raw)[kRows][kPPT],
   constexpr int kGroup = 64 / kRows;  // lanes holding one row's total
   const int rr = lane / kGroup;
   if constexpr (kWaves == 1) {
-    if (lane % kGroup == 0 && t.row0 + rr < t.nrows) {
+    if (live && lane % kGroup == 0 && t.row0 + rr < t.nrows) {
       const float v = acc[0] * out_scale;
       t.y[t.row0 + rr] = kAcc ? y_old + v : v;
     }
   } else {
     if (lane % kGroup == 0) red[wave][rr] = acc[0];
     __syncthreads();
-    if (tid < kRows && t.row0 + tid < t.nrows) {
+    if (live && tid < kRows && t.row0 + tid < t.nrows) {
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; w++) v += red[w][tid];
@@ -691,21 +695,29 @@ __device__ __forceinline__ void read_vec(float4 (&xv)[16], const uint8_t *lds, i
 
 using swamp::silu_mul;
 
-// One workgroup = 64 * kWaves lanes; lane j owns items j, j + T, ...
-// (kPPT items per lane), covering one row of ipr items.  The workgroup
-// walks tiles blockIdx.x, + gridDim.x, ... of kRows rows each.  Since every
-// workgroup holds all of x, a prologue that needs the whole vector (the
-// RMSNorm sum of squares) is computed by each workgroup for itself.
+// One row set = 64 * kWaves lanes; lane j owns items j, j + T, ... (kPPT
+// items per lane), covering one row of ipr items.  A workgroup is kSets row
+// sets that stage x once and then walk their own tiles: set s of workgroup
+// b takes tiles kSets b + s, + kSets gridDim.x, ... of kRows rows each.
+// One-wave sets need no barrier per tile and leave when their tiles end.
+// Sets of several waves sum a row through LDS behind a workgroup barrier,
+// so every set makes as many trips as set 0: a set past the last tile works
+// through a stand-in tile and stores nothing.  Since every workgroup holds
+// all of x, a prologue that needs the whole vector (the RMSNorm sum of
+// squares) is computed by each set for itself.
 // kX32: fp32 x (XFrag32, the reference's arithmetic); else x rounded to
 // fp16 (XFrag, dot2 arithmetic).
-template <int DT, int kPPT, int kRows, int kWaves, bool kMulti, int kPro, bool kX32>
-__global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const float *__restrict__ x,
-                                                           Pro pro, int ipr, size_t row_bytes,
-                                                           int n_tiles) {
+template <int DT, int kPPT, int kRows, int kWaves, bool kMulti, int kPro, bool kX32,
+          int kSets = 1>
+__global__ void __launch_bounds__(64 * kWaves * kSets)
+    gemv_kernel(MatSet ms, const float *__restrict__ x, Pro pro, int ipr, size_t row_bytes,
+                int n_tiles) {
   using XF = std::conditional_t<kX32, XFrag32<DT>, XFrag<DT>>;
   constexpr int T = 64 * kWaves;
-  __shared__ float red[2][kWaves][kRows];
-  const int tid = threadIdx.x;
+  constexpr bool kUniform = kSets > 1 && kWaves > 1;  // trips set by set 0
+  __shared__ float red[2][kSets][kWaves][kRows];
+  const int tid = kSets == 1 ? int(threadIdx.x) : int(threadIdx.x) % T;
+  const int set = kSets == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x) / T);
 
   int item[kPPT];
   bool valid[kPPT];
@@ -719,8 +731,15 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
 #pragma unroll
   for (int j = 0; j < kPPT; j++) off[j] = swamp::item_offset<DT>(item[j]);
 
-  int tile = blockIdx.x;
-  if (tile >= n_tiles) return;
+  // A set past the last tile still takes part in staging x (its loads
+  // re-read the last tile); a one-wave set then leaves after the staging
+  // barrier, a set of several waves keeps pace with set 0 on stand-in tiles.
+  const int stride = int(gridDim.x) * kSets;
+  int tile = int(blockIdx.x) * kSets + set;
+  const bool idle = tile >= n_tiles;
+  if (kSets == 1 && idle) return;
+  bool live_a = !idle;
+  if (idle) tile = n_tiles - 1;
   const uint32_t m = f16_magic();
 
   // x (and the prologue operand) first, then the first tile's weight loads,
@@ -735,12 +754,14 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
   constexpr bool kTwo = kStage && kPro != kProNone && kWaves <= 4;  // both vectors at once
   constexpr int kRegion = kWaves * 16384;
   __shared__ __align__(16) uint8_t xlds[kStage ? (kTwo ? 2 : 1) * kRegion : 16];
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  // waves of the workgroup and this wave's index among them (x staging)
+  constexpr int kWgWaves = kWaves * kSets;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)), lane = tid & 63;
   float4 x4[kPPT][16];
   [[maybe_unused]] float4 v4[kPPT][16];  // prologue operand (w_norm or up)
   if constexpr (kStage) {
-    stage_vec<DT, kWaves>(xlds, x, ipr, wave, lane);
-    if constexpr (kTwo) stage_vec<DT, kWaves>(xlds + kRegion, pro.x2, ipr, wave, lane);
+    stage_vec<DT, kWgWaves>(xlds, x, ipr, wave, lane);
+    if constexpr (kTwo) stage_vec<DT, kWgWaves>(xlds + kRegion, pro.x2, ipr, wave, lane);
   } else {
 #pragma unroll
     for (int j = 0; j < kPPT; j++) load_x<DT>(x4[j], x, item[j]);
@@ -768,7 +789,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
     } else if constexpr (kPro != kProNone) {
       // one region: the operand follows once every wave has read x
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      stage_vec<DT, kWaves>(xlds, pro.x2, ipr, wave, lane);
+      stage_vec<DT, kWgWaves>(xlds, pro.x2, ipr, wave, lane);
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
       read_vec(v4[0], xlds, item[0]);
     }
@@ -800,19 +821,20 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
         g = make_float4(g.x * w.x, g.y * w.y, g.z * w.z, g.w * w.w);
       }
   }
+  if (kSets > 1 && !kUniform && idle) return;  // after the workgroup's last barrier
   XF xf[kPPT];
 #pragma unroll
   for (int j = 0; j < kPPT; j++) build_xfrag<DT>(xf[j], x4[j], valid[j]);
   float out_scale = 1.0f;
   if constexpr (kPro == kProRmsNorm) {
-    __shared__ float ssq[kWaves];
+    __shared__ float ssq[kSets][kWaves];
     ss = swamp::wave_sum(ss);
     if (kWaves > 1) {
-      if ((tid & 63) == 0) ssq[tid >> 6] = ss;
+      if ((tid & 63) == 0) ssq[set][tid >> 6] = ss;
       __syncthreads();
       ss = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; w++) ss += ssq[w];
+      for (int w = 0; w < kWaves; w++) ss += ssq[set][w];
     }
     out_scale = __builtin_amdgcn_rsqf(ss / float(ipr * 64) + pro.eps);
   }
@@ -822,23 +844,36 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(MatSet ms, const floa
   // re-read the current one, already in cache), so every path through the
   // loop has the same number of loads in flight and the hardware wait
   // counts stay tight.
+  // Trip by trip, set s works on tile base + s, base advancing by stride
+  // (base is set 0's tile).  A one-wave set stops when its own next tile is
+  // past the end; with kUniform every set stops when set 0's is, a set
+  // whose tile is past the end working through a stand-in (its current
+  // tile, clamped) that it does not store.
+  int base = int(blockIdx.x) * kSets;
   for (;;) {
-    int nxt = tile + gridDim.x;
-    const TileRef tb = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
+    const int cur = tile;  // the tile ra holds (clamped)
+    int nb = base + stride;
+    bool live_b = nb + set < n_tiles;
+    const TileRef tb = tile_ref<kRows, kMulti>(ms, live_b ? nb + set : cur);
     issue_tile<DT, kPPT, kRows>(rb, tb, row_bytes, item, off);
     if constexpr (kAcc) yb = tb.y[store_row<kRows, kWaves>(tb, tid)];
     __builtin_amdgcn_sched_barrier(0);
-    consume_tile<DT, kPPT, kRows, kWaves, kAcc>(ra, xf, ta, item, red[0], tid, m, out_scale, ya);
-    if (nxt >= n_tiles) break;
-    tile = __builtin_amdgcn_readfirstlane(nxt);  // keep it scalar (no VGPR round trip)
-    nxt = tile + gridDim.x;
-    ta = tile_ref<kRows, kMulti>(ms, nxt < n_tiles ? nxt : tile);
+    consume_tile<DT, kPPT, kRows, kWaves, kAcc>(ra, xf, ta, item, red[0][set], tid, m, out_scale,
+                                                ya, live_a);
+    if (kUniform ? nb >= n_tiles : !live_b) break;
+    base = __builtin_amdgcn_readfirstlane(nb);  // keep it scalar (no VGPR round trip)
+    tile = live_b ? base + set : cur;           // the tile rb holds
+    nb = base + stride;
+    live_a = nb + set < n_tiles;
+    ta = tile_ref<kRows, kMulti>(ms, live_a ? nb + set : tile);
     issue_tile<DT, kPPT, kRows>(ra, ta, row_bytes, item, off);
     if constexpr (kAcc) ya = ta.y[store_row<kRows, kWaves>(ta, tid)];
     __builtin_amdgcn_sched_barrier(0);
-    consume_tile<DT, kPPT, kRows, kWaves, kAcc>(rb, xf, tb, item, red[1], tid, m, out_scale, yb);
-    if (nxt >= n_tiles) break;
-    tile = __builtin_amdgcn_readfirstlane(nxt);  // keep it scalar (no VGPR round trip)
+    consume_tile<DT, kPPT, kRows, kWaves, kAcc>(rb, xf, tb, item, red[1][set], tid, m, out_scale,
+                                                yb, live_b);
+    if (kUniform ? nb >= n_tiles : !live_a) break;
+    base = __builtin_amdgcn_readfirstlane(nb);  // keep it scalar (no VGPR round trip)
+    tile = live_a ? base + set : tile;          // the tile ra holds
   }
 }
 
@@ -858,11 +893,13 @@ bool item_path_ok(uint32_t dt, int n_cols) {
 struct Tuning {
   int waves_per_cu = 0;  // 0: chosen per shape
   int rows = 0;          // 0: chosen per shape
+  bool sets = true;      // row sets sharing x (SWAMP_GEMV_SETS=0 turns them off)
   Tuning() {
     if (const char *s = std::getenv("SWAMP_GEMV_WAVES_PER_CU")) {
       int v = std::atoi(s);
       if (v >= 1 && v <= 64) waves_per_cu = v;
     }
+    if (const char *s = std::getenv("SWAMP_GEMV_SETS")) sets = std::atoi(s) != 0;
     if (const char *s = std::getenv("SWAMP_GEMV_ROWS")) {
       int v = std::atoi(s);
       if (v == 1 || v == 2 || v == 4) rows = v;
@@ -874,23 +911,25 @@ const Tuning &tuning() {
   return t;
 }
 
-template <int DT, int kPPT, int kRows, int kWaves, int kPro, bool kX32>
+template <int DT, int kPPT, int kRows, int kWaves, int kPro, bool kX32, int kSets = 1>
 int launch_items(const MatSet &ms, const float *x, const Pro &pro, int n_cols, hipStream_t s) {
   const int ipr = n_cols / 64;
   if (ipr > kPPT * 64 * kWaves) return SWAMP_ESHAPE;
   const int n_tiles = ms.tile_end[ms.n - 1];
   const int cus = swamp::device_info().num_cus;
-  int grid = cus * std::max(1, ms.wpc / kWaves);
-  if (grid > n_tiles) grid = n_tiles;
+  int grid = cus * std::max(1, ms.wpc / (kWaves * kSets));
+  const int need = (n_tiles + kSets - 1) / kSets;  // workgroups with a tile for set 0
+  if (grid > need) grid = need;
   if (grid < 1) return SWAMP_OK;
+  constexpr int kThreads = 64 * kWaves * kSets;
   if (ms.n == 1)
-    gemv_kernel<DT, kPPT, kRows, kWaves, false, kPro, kX32>
-        <<<grid, 64 * kWaves, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
+    gemv_kernel<DT, kPPT, kRows, kWaves, false, kPro, kX32, kSets>
+        <<<grid, kThreads, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
   else if constexpr (kPro == kProSwiGLU || kPro == kProSwiGLUAcc)
     return SWAMP_EINVAL;  // single matrix only
   else
-    gemv_kernel<DT, kPPT, kRows, kWaves, true, kPro, kX32>
-        <<<grid, 64 * kWaves, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
+    gemv_kernel<DT, kPPT, kRows, kWaves, true, kPro, kX32, kSets>
+        <<<grid, kThreads, 0, s>>>(ms, x, pro, ipr, swamp::row_bytes(DT, n_cols), n_tiles);
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
 
@@ -898,6 +937,7 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
                  int tile_rows) {
   ms.n = n;
   ms.wpc = 4;
+  ms.sets = tuning().sets;
   int acc = 0;
   for (int i = 0; i < n; i++) {
     ms.w[i] = static_cast<const uint8_t *>(ws[i]);
@@ -913,14 +953,13 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
 int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
 
 // Waves per CU of the persistent grid: 4 (one per SIMD); 8 for the fp32-x
-// Q4_0 / Q4_K kernels on large matrices (at least 16384 rows, or rows of
-// more than 4096 weights), whose heavier arithmetic per weight needs a
-// second wave per SIMD to keep loads in flight (measured sweep, 8B
-// shapes: gate+up 17.0 -> 15.5 us, down 10.6 -> 9.8 us, Q4_K lm_head
-// 64.4 -> 60.3 us).
+// Q4_0 / Q4_K kernels on the larger matrices (at least 6144 rows, or rows
+// of more than 4096 weights), whose heavier arithmetic per weight needs a
+// second wave per SIMD to keep loads in flight.  With 2-row tiles, 6144
+// rows are then at most two tiles per wave, all in flight from the start.
 int waves_per_cu_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   if (tuning().waves_per_cu) return tuning().waves_per_cu;
-  if (x32 && (dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && (total_rows >= 16384 || n_cols > 4096))
+  if (x32 && (dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && (total_rows >= 6144 || n_cols > 4096))
     return 8;
   return 4;
 }
@@ -939,9 +978,9 @@ int tile_rows_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   if (dt == SWAMP_Q6_K) cap = ipr <= 256 ? 2 : 1;
   // Q8_0 with fp32 x: the register budget allows 2 rows
   if (dt == SWAMP_Q8_0 && x32) cap = std::min(cap, 2);
+  if (tuning().rows) return std::min(tuning().rows, cap);
   const int wpc = waves_per_cu_for(dt, n_cols, total_rows, x32);
   if (wpc >= 8) cap = std::min(cap, 2);
-  if (tuning().rows) return std::min(tuning().rows, cap);
   const int cus = swamp::device_info().num_cus;
   const long slots = long(cus) * std::max(1, wpc / waves_for(ipr));
   int r = 1;
@@ -959,8 +998,20 @@ int launch_rows(const MatSet &ms, const float *x, const Pro &pro, int n_cols, hi
   if constexpr (kRows > 2 && (DT == SWAMP_Q6_K || (kX32 && DT == SWAMP_Q8_0))) {
     return SWAMP_ESHAPE;
   } else {
-    if (ipr <= 64) return launch_items<DT, 1, kRows, 1, kPro, kX32>(ms, x, pro, n_cols, s);
-    if (ipr <= 128) return launch_items<DT, 1, kRows, 2, kPro, kX32>(ms, x, pro, n_cols, s);
+    // row sets sharing x: 4 sets of one wave, 2 of two waves (when the grid
+    // aims for 8 waves per CU).  Measured per matrix, fp32 x (us, sets /
+    // none): 8B Q4_0 qkv 5.97 / 6.31, o_proj 4.55 / 5.08, gate_up 13.79 /
+    // 15.14, lm_head 52.2 / 56.5; 70B Q4_K qkv 12.4 / 13.3, gate_up 52.1 /
+    // 58.2.  Two sets of four waves (K = 14336) measured slower (down 10.1
+    // / 9.9): their barrier per tile ties the two sets together.
+    if (ipr <= 64) {
+      if (ms.sets) return launch_items<DT, 1, kRows, 1, kPro, kX32, 4>(ms, x, pro, n_cols, s);
+      return launch_items<DT, 1, kRows, 1, kPro, kX32>(ms, x, pro, n_cols, s);
+    }
+    if (ipr <= 128) {
+      if (ms.sets && ms.wpc >= 8) return launch_items<DT, 1, kRows, 2, kPro, kX32, 2>(ms, x, pro, n_cols, s);
+      return launch_items<DT, 1, kRows, 2, kPro, kX32>(ms, x, pro, n_cols, s);
+    }
     if (ipr <= 256) return launch_items<DT, 1, kRows, 4, kPro, kX32>(ms, x, pro, n_cols, s);
     if (ipr <= 512) return launch_items<DT, 1, kRows, 8, kPro, kX32>(ms, x, pro, n_cols, s);
     // the fused prologues keep one item per lane (n_cols <= 32768)

@@ -170,6 +170,17 @@ def test_gemv_parity_small_blocks(pkg, orc, torch_dev, dtype, cols):
     _gemv_check(pkg, orc, torch_dev, dtype, 129, cols)
 
 
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (3, 4096), (6, 4096), (4099, 4096),
+                                       (6150, 4096), (5, 8192), (4097, 8192), (16387, 8192)])
+def test_gemv_row_sets(pkg, orc, torch_dev, dtype, rows, cols):
+    # Rows of at most 128 items run as several row sets per workgroup sharing
+    # x (one-wave sets for K = 4096, two-wave sets with workgroup-uniform
+    # trips for K = 8192); these row counts leave sets of the last
+    # workgroups without a tile, or with one trip fewer than set 0.
+    _gemv_check(pkg, orc, torch_dev, dtype, rows, cols, mid=rows)
+
+
 @pytest.mark.parametrize("dtype", [Q4_0, Q4_K])
 def test_gemv_8b_shapes_subsets(pkg, orc, torch_dev, dtype):
     for rows, cols in [(6144, 4096), (28672, 4096), (128256, 4096)]:

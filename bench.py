@@ -412,6 +412,71 @@ def run_sweep(pkg, torch, np, stream, lib):
           flush=True)
 
 
+ROUTE_SHAPES = [("gate_up", 28672, 4096), ("down", 4096, 14336), ("qkv", 6144, 4096),
+                ("o_proj", 4096, 4096)]
+ROUTE_MS = (256, 512, 1024, 2048)
+
+
+def route_times(pkg, torch, s):
+    """us per swamp_qgemm call (Q4_0 weights, bf16 x; mean of 20 after 10
+    warm-up calls) for each 8B shape and prompt length, through whichever
+    route SWAMP_GEMM_ROUTE forces in this process."""
+    import numpy as np
+    lib = pkg.gpu_lib()
+    out = {}
+    for i, (name, rows, k) in enumerate(ROUTE_SHAPES):
+        w = torch.from_numpy(pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x300 ^ i, 0.02, rows, k)).cuda()
+        for m in ROUTE_MS:
+            xb = torch.from_numpy(pkg.to_bf16_bits(pkg.fill_normal(SEED ^ 0x400 ^ m, 1.0, m, k))
+                                  .view(np.int16)).cuda()
+            y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+
+            def call():
+                rc = lib.swamp_qgemm(pkg.Q4_0, w.data_ptr(), w.numel(), xb.data_ptr(), pkg.BF16,
+                                     y.data_ptr(), m, rows, k, s)
+                if rc != 0:
+                    raise pkg.GpuError(rc, "swamp_qgemm")
+            for _ in range(10):
+                call()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(20):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            out[f"{name}@{m}"] = round(e0.elapsed_time(e1) * 1e3 / 20, 1)
+    return out
+
+
+def route_crossover():
+    """The prefill GEMM's two routes side by side: each timed in a child
+    process with SWAMP_GEMM_ROUTE set (the library reads it once)."""
+    import subprocess
+    res = {}
+    for route in ("fused", "dq"):
+        env = dict(os.environ, SWAMP_GEMM_ROUTE=route)
+        p = subprocess.run([sys.executable, os.path.abspath(__file__), "--route-times"], env=env,
+                           capture_output=True, text=True, timeout=600)
+        if p.returncode != 0:
+            raise SystemExit(f"route {route}: child failed ({p.returncode}): {p.stderr[-2000:]}")
+        res[route] = json.loads([ln for ln in p.stdout.splitlines() if ln.startswith("{")][-1])
+    table = []
+    for name, rows, k in ROUTE_SHAPES:
+        for m in ROUTE_MS:
+            key = f"{name}@{m}"
+            flop = 2.0 * m * rows * k
+            table.append({"name": name, "m": m, "rows": rows, "k": k,
+                          "fused_us": res["fused"][key], "dq_us": res["dq"][key],
+                          "faster": "dq" if res["dq"][key] < res["fused"][key] else "fused",
+                          "best_frac_bf16_peak": round(flop / (min(res["dq"][key],
+                                                                   res["fused"][key]) * 1e-6)
+                                                       / 1e12 / BF16_PEAK_TFLOPS, 4)})
+    print(json.dumps({"route_crossover": "swamp_qgemm Q4_0, bf16 x, 8B shapes; mean of 20 calls "
+                                         "after 10 warm-up calls per route",
+                      "shapes": table}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -432,6 +497,11 @@ def main():
                     help="only run 5 calls of the 2048-token gate+up prefill GEMM (Q4_0 weights; "
                          "x bf16, or int8: x quantized to Q8_0 on the device, then the int8 "
                          "GEMM) and one 256 MiB device copy (for rocprofv3 --pmc), no JSON")
+    ap.add_argument("--route-crossover", action="store_true",
+                    help="only time swamp_qgemm (Q4_0, bf16 x) at 256..2048 tokens on the 8B "
+                         "shapes through each prefill route, forced with SWAMP_GEMM_ROUTE in two "
+                         "child processes; one JSON line")
+    ap.add_argument("--route-times", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
@@ -443,6 +513,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.route_crossover:
+        route_crossover()
+        return
+
     import numpy as np
     import torch
 
@@ -453,6 +527,10 @@ def main():
     pkg.init()
     stream = torch.cuda.current_stream()
     s = stream.cuda_stream
+
+    if args.route_times:
+        print(json.dumps(route_times(pkg, torch, s)), flush=True)
+        return
 
     # ---- data: one host-quantized weight set, cloned on the device -------
     sets = [[] for _ in range(args.copies)]

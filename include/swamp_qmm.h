@@ -207,15 +207,19 @@ SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     weights only; n_cols a multiple of 128.
  * dtype Q4_0, Q8_0, Q4_K or Q6_K (Q4_K and Q6_K with bf16 x only); bf16 x
  * needs n_cols a multiple of 64.
- * Below 2048 tokens (bf16 x) the fused kernel dequantizes weight tiles in
+ * Below 1024 tokens (bf16 x) the fused kernel dequantizes weight tiles in
  * registers to bf16; when the tiles do not fill the GPU, K is split across
  * workgroups whose partial tiles go to scratch and are summed in piece
- * order by a second kernel (deterministic).  From 2048 tokens, and for Q6_K
- * at any length, the weights are dequantized once per call to bf16 in
- * scratch (row chunks of at most 128 MB; the same bf16 values) and each
- * chunk is multiplied by a hipBLASLt bf16 GEMM with fp32 accumulation; when
- * that scratch cannot be had the fused kernel runs (Q6_K:
- * SWAMP_EWORKSPACE). */
+ * order by a second kernel (deterministic).  From 1024 tokens (matrices of
+ * at least 1024 x 1024), and for Q6_K at any length, the weights are
+ * dequantized once per call to bf16 in scratch (row chunks of at most
+ * 128 MB; the same bf16 values) and each chunk is multiplied by a hipBLASLt
+ * bf16 GEMM with fp32 accumulation; when that scratch cannot be had the
+ * fused kernel runs (Q6_K: SWAMP_EWORKSPACE).  The first such call of a
+ * shape on a device measures the library's candidate algorithms on its
+ * stream and keeps the fastest (a one-time step that waits for the stream;
+ * skipped under graph capture and with SWAMP_GEMM_TUNE=0); the choice may
+ * differ between processes, and with it the order of the fp32 sums. */
 SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);

@@ -36,7 +36,8 @@ Also reported (outside the timed steps):
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--cpu-threads 6,max] [--sweep] [--pmc-probe] [--pmc-gemm]
 --sweep adds one JSON line per extra workload after the main line: the
-Q4_K small-batch sweep (1/4/8/16 tokens) at 8B shapes and the 70B layer
+Q4_K small-batch sweep (1/4/8/16/17/24/32/64 tokens; more than 16 take the
+prefill-GEMM route) at 8B shapes and the 70B layer
 (decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
 --pmc-gemm the same for the 2048-token gate+up prefill GEMM.
@@ -307,7 +308,7 @@ def run_sweep(pkg, torch, np, stream, lib):
             raise pkg.GpuError(rc, what)
 
     for label, shapes, sigma in (("llama3-8b", SWEEP_8B, 0.02), ("llama3-70b", SWEEP_70B, 0.015)):
-        for n_tok in ((1, 4, 8, 16, 64) if label == "llama3-8b" else (1,)):
+        for n_tok in ((1, 4, 8, 16, 17, 24, 32, 64) if label == "llama3-8b" else (1,)):
             per, tot_b, tot_us = [], 0, 0.0
             for i, (name, rows, k) in enumerate(shapes):
                 dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K

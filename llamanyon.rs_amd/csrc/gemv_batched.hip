@@ -48,7 +48,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kTok = 16;        // tokens per pass (MFMA M)
 constexpr int kRowsTile = 16;   // rows per tile (MFMA N)
 constexpr int kJmax = 2;        // tiles per wave whose accumulators stay in registers
-constexpr int kXLdsMax = 131072;             // activation bytes in LDS (one K phase)
+constexpr int kXLdsMax = 139264;             // activation bytes in LDS (one K phase)
 constexpr int kSlotBytes = kWaves * 16 * 16 * 4;  // one 16x16 fp32 partial per wave
 constexpr uint32_t kF16Magic = 0x64006400u;  // fp16 pair (1024, 1024)
 constexpr uint32_t kOob = 0x80000000u;       // buffer offset past any descriptor: reads 0
@@ -276,20 +276,42 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Stage the activations of items [item0, item0 + n_items) into LDS: entry
-// e = (item, step, token) with the token fastest, so the LDS writes are
-// linear; missing tokens and items past the row are zero.  kU entries per
-// thread are loaded before any is written, so the loads overlap (fewer
-// inside the main loop, where both weight chunks hold registers).
+// Stage the activations of items [item0, item0 + n_items) into LDS as
+// fragments: entry (item, step, token) holds the 8 fp16 values one lane
+// feeds one MFMA, at row 8 * item + step, slot token; rows are TOK + 1
+// slots long (one slot of padding), which spreads both the staging writes
+// (consecutive rows) and the MFMA reads (consecutive tokens) over the banks.
+// Thread e takes step e % 8 of item (e / 8) % n_items of token e / (8 *
+// n_items): consecutive threads read consecutive 32-byte runs of one
+// token's x, so a wave's loads cover whole cache lines (the token-fastest
+// order read 16 rows per instruction, 64 bytes of each line, and staging
+// took most of a 16-token pass).  Missing tokens and items past the row
+// are zero.  kU entries per thread are loaded before any is written, so the
+// loads overlap (fewer inside the main loop, where both weight chunks hold
+// registers).
+template <int TOK>
+constexpr int frag_row() { return TOK + 1; }  // 16-byte slots per fragment row
+// r / n for r < 2^24, n > 0: the float quotient is within one of the
+// integer one, which one correction each way makes exact (no integer
+// division sequence, whose temporaries would hold registers while the
+// first weight chunk is in flight).
+__device__ __forceinline__ int div_small(int r, int n, float inv_n) {
+  int q = int(float(r) * inv_n);
+  q -= q * n > r ? 1 : 0;
+  q += (q + 1) * n <= r ? 1 : 0;
+  return q;
+}
 template <int DT, int TOK, int kU>
 __device__ __forceinline__ void stage_x(const Args &a, half8_t *xl, int item0, int n_items, int tid) {
   const int n_ent = n_items * 8 * TOK;
+  const float inv_n = 1.0f / float(n_items);
   for (int e0 = tid; e0 < n_ent; e0 += kU * kThreads) {
     float4 v0[kU], v1[kU];
 #pragma unroll
     for (int u = 0; u < kU; u++) {
       const int e = e0 + u * kThreads;
-      const int tok = e % TOK, st = (e / TOK) & 7, item = item0 + e / (8 * TOK);
+      const int st = e & 7, r = e >> 3, tok = div_small(r, n_items, inv_n);
+      const int item = item0 + (r - tok * n_items);
       v0[u] = v1[u] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (e < n_ent && tok < a.n_tok && item < a.ipr) {
         const float *xp = a.x + size_t(tok) * a.n_cols + size_t(item) * 64;
@@ -305,7 +327,8 @@ __device__ __forceinline__ void stage_x(const Args &a, half8_t *xl, int item0, i
         half8_t h;
 #pragma unroll
         for (int i = 0; i < 8; i++) h[i] = _Float16(v[slot_local<DT>(i)]);
-        xl[e] = h;
+        const int r = e >> 3, tok = div_small(r, n_items, inv_n);
+        xl[(8 * (r - tok * n_items) + (e & 7)) * frag_row<TOK>() + tok] = h;
       }
     }
   }
@@ -347,7 +370,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   const uint32_t rb = a.row_bytes;
   const uint32_t lane_off = uint32_t(r16) * rb + lane_item_offset<DT>(g);
   const uint32_t chunk_bytes = kChunk * quad_bytes<DT>();
-  float *slots = reinterpret_cast<float *>(xl + ipp * 8 * TOK);  // [16 waves][16 tok][16 rows]
+  float *slots = reinterpret_cast<float *>(xl + ipp * 8 * frag_row<TOK>());  // [16 waves][16 tok][16 rows]
 
   auto tile_of = [&](int batch, int j) { return (b + (batch * kJmax + j) * G) * wt + tl; };
   auto batch_len = [&](int batch) { return min(kJmax, J - batch * kJmax); };
@@ -402,7 +425,10 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   stage_x<DT, TOK, 4>(a, xl, kitem0, ipp, tid);
   __syncthreads();
 
-  const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * TOK + (r16 % TOK);
+  // this lane's fragments: rows 8 * item + step of its items (item
+  // ks * ipw + g + 4 j), slot r16 % TOK
+  constexpr int FR = frag_row<TOK>();
+  const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * FR + (r16 % TOK);
   // accumulators of the batch's tiles (named registers: an indexed array
   // would live in scratch, whose accesses share the vector memory counter
   // with the weight prefetch and drain it)
@@ -447,7 +473,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       stage_x<DT, TOK, 1>(a, xl, kitem0 + qc.p * ipp, ipp, tid);
       lds_barrier();
     }
-    const half8_t *xc = xlane + qc.c * kChunk * 32 * TOK;
+    const half8_t *xc = xlane + qc.c * kChunk * 32 * FR;
     float4_t c = acc0;
 #pragma unroll
     for (int i = 0; i < kChunk; i++) {
@@ -455,7 +481,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       if constexpr (DT == SWAMP_Q4_K) kq = q4k_item_scales(r[i], g);
 #pragma unroll
       for (int st = 0; st < 8; st++) {
-        const half8_t xa = xc[i * 32 * TOK + st * TOK];
+        const half8_t xa = xc[(i * 32 + st) * FR];
         const half8_t wb = weights_step<DT>(r[i], st, kq);
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, c, 0, 0, 0);
       }
@@ -517,7 +543,7 @@ int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, kXLdsMax + kSlotBytes);
   });
   const int q = 4 * kChunk;                           // item granule of a wave's K slice
-  const int xcap = kXLdsMax / (TOK * 8 * 16);         // items of activations in LDS
+  const int xcap = kXLdsMax / (frag_row<TOK>() * 8 * 16);  // items of activations in LDS
   const int wk = 1 << lwk;
   const int gran = q * wk;
   int ipp;
@@ -540,7 +566,7 @@ int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
   const int n_tg = (n_tiles + (kWaves >> lwk) - 1) / (kWaves >> lwk);
   const int grid = (a.nkg > 1 ? n_tg : std::min(n_tg, swamp::device_info().num_cus)) * a.nkg;
-  const size_t lds = size_t(ipp) * 8 * TOK * 16 + (wk > 1 ? kSlotBytes : 0);
+  const size_t lds = size_t(ipp) * 8 * frag_row<TOK>() * 16 + (wk > 1 ? kSlotBytes : 0);
   kern<<<unsigned(grid), kThreads, lds, s>>>(a);
   if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
   if (a.nkg > 1) {
@@ -573,7 +599,7 @@ KgPlan kg_plan(int n_tok, int n_rows, int n_cols, int tok) {
   const int ipr = (n_cols + 63) / 64;
   const int cus = swamp::device_info().num_cus;
   const int n_tg0 = ((n_rows + kRowsTile - 1) / kRowsTile + kWaves - 1) / kWaves;
-  const int xcap_items = kXLdsMax / (tok * 8 * 16);
+  const int xcap_items = kXLdsMax / ((tok + 1) * 8 * 16);
   if (forced == 1) return {1, 8};
   if (forced <= 0 && (2 * n_tg0 > cus || long(n_tok) * n_cols < kKgMinX)) return {1, 8};
   KgPlan best{1, 8};
@@ -598,7 +624,7 @@ template <int DT, int TOK>
 int launch_pass_tok(Args a, hipStream_t s) {
   const int cus = swamp::device_info().num_cus;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
-  const int xcap = kXLdsMax / (TOK * 8 * 16);
+  const int xcap = kXLdsMax / (frag_row<TOK>() * 8 * 16);
   if (a.ws) {
     const KgPlan kp = kg_plan(a.n_tok, a.n_rows, a.n_cols, TOK);
     const int nkg = kp.nkg, q = kp.q;

@@ -953,14 +953,20 @@ int build_matset(MatSet &ms, int n, const void *const *ws, float *const *ys, con
 int waves_for(int ipr) { return ipr <= 64 ? 1 : ipr <= 128 ? 2 : ipr <= 256 ? 4 : 8; }
 
 // Waves per CU of the persistent grid: 4 (one per SIMD); 8 for the fp32-x
-// Q4_0 / Q4_K kernels on the larger matrices (at least 6144 rows, or rows
-// of more than 4096 weights), whose heavier arithmetic per weight needs a
-// second wave per SIMD to keep loads in flight.  With 2-row tiles, 6144
-// rows are then at most two tiles per wave, all in flight from the start.
+// kernels on the larger matrices, whose heavier arithmetic per weight needs
+// a second wave per SIMD to keep loads in flight: Q4_0 / Q4_K from 6144
+// rows (with 2-row tiles at most two tiles per wave, all in flight from the
+// start), Q6_K from 16384 rows, and all three, and Q8_0, for rows of more
+// than 4096 weights.  Measured (bench.py --sweep, us, 4 -> 8 waves per
+// CU): Q6_K lm_head 128256 x 4096 84.0 -> 75.4, gate_up 21.6 -> 20.3, down
+// 17.0 -> 16.1, qkv 7.6 -> 7.7; Q8_0 lm_head 128256 x 8192 199.4 -> 181.9,
+// 128256 x 4096 90.1 -> 92.1.
 int waves_per_cu_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   if (tuning().waves_per_cu) return tuning().waves_per_cu;
-  if (x32 && (dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && (total_rows >= 6144 || n_cols > 4096))
-    return 8;
+  if (!x32) return 4;
+  if (n_cols > 4096) return 8;
+  if ((dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && total_rows >= 6144) return 8;
+  if (dt == SWAMP_Q6_K && total_rows >= 16384) return 8;
   return 4;
 }
 

@@ -57,22 +57,25 @@ __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast
 __device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 // Element (0..63 of the item) that operand slot i (0..7) of MFMA step st
-// (0..7) multiplies.  Slot i = pair i/2, half i%2; pair p of a nibble dword
-// holds the nibbles at bit offsets 4p and 4p+16 (P0..P3 = w>>0,4,8,12).
+// (0..7) multiplies.  Q4: a step's nibble dword splits into the bytes'
+// low nibbles (slots 0..3) and high nibbles (slots 4..7), two fp16 pairs
+// each, in byte order.  Q8_0: pair p of the step's two int8 dwords holds
+// bytes (0, 2) or (1, 3) of one dword.
 template <int DT>
 __host__ __device__ constexpr int slot_elem(int st, int i) {
-  const int p = i / 2, h = i % 2;
   if (DT == SWAMP_Q8_0) {
+    const int p = i / 2, h = i % 2;
     // two int8 dwords per step; pair 0/1 of dword 0 -> bytes (0,2), (1,3)
     const int dw = p / 2, pb = p % 2;
     const int byte = pb + 2 * h;
     return 32 * (st / 4) + 8 * (st % 4) + 4 * dw + byte;
   }
-  const int n = p + 4 * h;  // nibble index in the dword (bit 4n)
-  if (DT == SWAMP_Q4_0) return 32 * (st / 4) + 8 * (st % 4) + n;  // interleaved: nibble n = element n
+  const int hi = i / 4, byte = i % 4;
+  // Q4_0: nibble n of a dword is element n (low nibble of byte b: 2b)
+  if (DT == SWAMP_Q4_0) return 32 * (st / 4) + 8 * (st % 4) + 2 * byte + hi;
   // Q4_K quarter: dword st = bytes 4st..4st+3; low nibble -> sub-block A
   // element 4st + byte, high nibble -> sub-block B (item elements 32..63)
-  return 32 * (n % 2) + 4 * st + n / 2;
+  return 32 * hi + 4 * st + byte;
 }
 
 // The 8 elements of step st, as loaded by the activation staging: Q4_0 and
@@ -85,11 +88,12 @@ __host__ __device__ constexpr int stage_elem(int st, int v) {
 }
 template <int DT>
 __host__ __device__ constexpr int slot_local(int i) {
-  const int p = i / 2, h = i % 2;
-  if (DT == SWAMP_Q8_0) return 4 * (p / 2) + (p % 2) + 2 * h;
-  const int n = p + 4 * h;
-  if (DT == SWAMP_Q4_0) return n;
-  return 4 * (n % 2) + n / 2;
+  if (DT == SWAMP_Q8_0) {
+    const int p = i / 2, h = i % 2;
+    return 4 * (p / 2) + (p % 2) + 2 * h;
+  }
+  if (DT == SWAMP_Q4_0) return 2 * (i % 4) + i / 4;
+  return i;
 }
 template <int DT>
 constexpr bool staging_matches_slots() {
@@ -139,8 +143,27 @@ __device__ __forceinline__ Q4kScales q4k_item_scales(const Raw<SWAMP_Q4_K> &r, i
   return s;
 }
 
+// The nibbles 0..15 of a dword's four bytes as exact fp16 pairs: the
+// low nibbles (lo[0] = bytes 0,1; lo[1] = bytes 2,3), then the high ones.
+// A byte below 16 read as OCP fp8 E4M3 is that integer times 2^-9 (the
+// denormals run on linearly into the first binade); the convert's scale
+// operand contributes its power of two, 2^9, so the pairs are the nibbles
+// themselves: 4 converts and 3 bit operations per 8 weights.
+struct Nib8 {
+  half2_t lo[2], hi[2];
+};
+__device__ __forceinline__ Nib8 nibbles_f16(uint32_t w) {
+  const uint32_t l = w & 0x0F0F0F0Fu, h = (w >> 4) & 0x0F0F0F0Fu;
+  Nib8 n;
+  n.lo[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l, 512.0f, false);
+  n.lo[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l, 512.0f, true);
+  n.hi[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h, 512.0f, false);
+  n.hi[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h, 512.0f, true);
+  return n;
+}
+
 // 8 fp16 weights (4 packed dwords) of MFMA step st from one item (for
-// Q4_K with its scales from q4k_item_scales).
+// Q4_K with its scales from q4k_item_scales), in slot_elem order.
 template <int DT>
 __device__ __forceinline__ half8_t weights_step(const Raw<DT> &r, int st, const Q4kScales &ks) {
   uint32_t o[4];
@@ -149,12 +172,13 @@ __device__ __forceinline__ half8_t weights_step(const Raw<DT> &r, int st, const 
     const uint32_t w = blk == 0 ? shr16(r.d[t + 1], r.d[t]) : r.d[5 + t];
     const uint32_t dbits = blk == 0 ? (r.d[0] & 0xFFFFu) : (r.d[4] >> 16);
     const half2_t d2 = as_h2(dbits | (dbits << 16));
-    const half2_t off = {_Float16(-1032.0f), _Float16(-1032.0f)};
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const uint32_t P = ((w >> (4 * p)) & 0x000F000Fu) | kF16Magic;
-      o[p] = as_u((as_h2(P) + off) * d2);  // (q - 8) exact, then one rounding
-    }
+    const half2_t m8 = d2 * half2_t{_Float16(-8.0f), _Float16(-8.0f)};  // exact
+    const Nib8 n = nibbles_f16(w);
+    // (q - 8) * d rounded once, as fma(q, d, -8d)
+    o[0] = as_u(__builtin_elementwise_fma(n.lo[0], d2, m8));
+    o[1] = as_u(__builtin_elementwise_fma(n.lo[1], d2, m8));
+    o[2] = as_u(__builtin_elementwise_fma(n.hi[0], d2, m8));
+    o[3] = as_u(__builtin_elementwise_fma(n.hi[1], d2, m8));
   } else if constexpr (DT == SWAMP_Q8_0) {
     const int blk = st / 4, t = st % 4;
     uint32_t w0, w1, dbits;
@@ -179,16 +203,12 @@ __device__ __forceinline__ half8_t weights_step(const Raw<DT> &r, int st, const 
     o[2] = as_u((as_h2(__builtin_amdgcn_perm(mg, u1, kSelEven)) + off) * d2);
     o[3] = as_u((as_h2(__builtin_amdgcn_perm(mg, u1, kSelOdd)) + off) * d2);
   } else {
-    const half2_t off = {_Float16(-1024.0f), _Float16(-1024.0f)};
-    const uint32_t w = r.q[st];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-      // pair p: nibbles at bits 4p and 4p+16; p even -> low nibbles (A)
-      const uint32_t P = ((w >> (4 * p)) & 0x000F000Fu) | kF16Magic;
-      const half2_t q = as_h2(P) + off;
-      const bool a = (p % 2) == 0;
-      o[p] = as_u(q * (a ? ks.sa : ks.sb) - (a ? ks.ma : ks.mb));
-    }
+    const Nib8 n = nibbles_f16(r.q[st]);
+    // q * s - m rounded once per weight; low nibbles sub-block A, high B
+    o[0] = as_u(__builtin_elementwise_fma(n.lo[0], ks.sa, -ks.ma));
+    o[1] = as_u(__builtin_elementwise_fma(n.lo[1], ks.sa, -ks.ma));
+    o[2] = as_u(__builtin_elementwise_fma(n.hi[0], ks.sb, -ks.mb));
+    o[3] = as_u(__builtin_elementwise_fma(n.hi[1], ks.sb, -ks.mb));
   }
   half8_t v;
 #pragma unroll

@@ -35,12 +35,14 @@ Also reported (outside the timed steps):
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--cpu-threads 6,max] [--sweep] [--pmc-probe] [--pmc-gemm]
+                       [--pmc-batched N]
 --sweep adds one JSON line per extra workload after the main line: the
 Q4_K small-batch sweep (1/4/8/16/17/24/32/64 tokens; more than 16 take the
 prefill-GEMM route) at 8B shapes and the 70B layer
 (decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
---pmc-gemm the same for the 2048-token gate+up prefill GEMM.
+--pmc-gemm the same for the 2048-token gate+up prefill GEMM; --pmc-batched N
+runs 5 small-batch launches of N tokens per 8B sweep matrix, for counter passes.
 """
 from __future__ import annotations
 
@@ -494,6 +496,9 @@ def main():
     ap.add_argument("--sweep", action="store_true",
                     help="also print one line per extra workload (8B small-batch Q4_K sweep, "
                          "70B decode and prefill) after the main line")
+    ap.add_argument("--pmc-batched", type=int, default=0, metavar="N",
+                    help="only run 5 swamp_qgemv_batched launches of N tokens on each 8B sweep "
+                         "matrix (Q4_K, lm_head Q8_0), for rocprofv3 --pmc counter passes; no JSON")
     ap.add_argument("--pmc-gemm", nargs="?", const="bf16", choices=["bf16", "int8"],
                     help="only run 5 calls of the 2048-token gate+up prefill GEMM (Q4_0 weights; "
                          "x bf16, or int8: x quantized to Q8_0 on the device, then the int8 "
@@ -581,6 +586,25 @@ def main():
         torch.cuda.synchronize()
         print(f"pmc gemm: 5 x swamp_qgemm Q4_0 {name} {pm}x{rows}x{k} ({args.pmc_gemm} x), then a "
               f"{src.numel()}-byte device copy", flush=True)
+        return
+
+    if args.pmc_batched:
+        # the small batch under rocprofv3 --pmc: 5 launches per 8B matrix,
+        # in sweep order, each matrix with its own weights and activations
+        n_tok = args.pmc_batched
+        for i, (name, rows, k) in enumerate(SWEEP_8B):
+            dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
+            w = torch.from_numpy(pkg.synth_quantized(dt, SEED ^ 0x300 ^ i, 0.02, rows, k)).cuda()
+            x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x400 ^ i, 1.0, n_tok, k)).cuda()
+            y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+            for _ in range(5):
+                rc = lib.swamp_qgemv_batched(dt, w.data_ptr(), w.numel(), x.data_ptr(), y.data_ptr(),
+                                             n_tok, rows, k, 0, s)
+                if rc != 0:
+                    raise pkg.GpuError(rc, "swamp_qgemv_batched")
+            torch.cuda.synchronize()
+            print(f"pmc batched: 5 x swamp_qgemv_batched {name} {rows}x{k} n_tok {n_tok}", flush=True)
+            del w, x, y
         return
 
     if args.pmc_probe:

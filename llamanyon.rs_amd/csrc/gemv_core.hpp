@@ -326,26 +326,49 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag<DT> &xf,
 // ---- fp32 x: the reference's arithmetic ------------------------------------
 // The default GEMV multiplies the exact weight codes by unrounded fp32 x and
 // sums in fp32, as forward_linear (linear.rs:81-85) and the scalar Q4_K
-// GEMV (fused_gemv_q4k.rs:484-504) do.  A weight pair still becomes an fp16
-// pair with one and-or (1024 + q, or 1024 + 16 q for a nibble left in
-// place); one packed fp16 add or fma then removes the magic offset, which
-// is exact (the results are small integers), leaving the signed code
-// (q - 8 for Q4_0, q for Q4_K, q - 32 for Q6_K).  V_FMA_MIX_F32 converts
-// each half to fp32 (exact) and fuses it with the fp32 x value and the fp32
-// partial sum: one rounding per weight, as in an fp32 FMA.  Q8_0 bytes are
-// converted with a sign-extending sub-dword convert.  The block scales are
-// applied per block (Q4_0, Q8_0, Q6_K: d * sum; Q4_K: (d sc) sum(q x) -
-// (dmin m) sum(x), with sum(x) per sub-block taken once per lane).
-// Per 8 nibbles: 1 shift + 4 and-or + 4 packed fp16 ops + 8 fma_mix.
+// GEMV (fused_gemv_q4k.rs:484-504) do.  Q4_0 and Q4_K nibbles become their
+// exact codes q as fp16 pairs through the fp8 convert (nib4_f16); Q6_K
+// pairs take one and-or onto the fp16 magic (1024 + q, or 1024 + 16 q for a
+// nibble left in place) and one packed fp16 add or fma that removes it,
+// exactly, leaving q - 32.  V_FMA_MIX_F32 converts each half to fp32
+// (exact) and fuses it with the fp32 x value and the fp32 partial sum: one
+// rounding per weight, as in an fp32 FMA.  Q8_0 bytes are converted with a
+// sign-extending sub-dword convert.  The block scales and offsets are
+// applied per block: Q4_0 d (sum(q x) - 8 sum(x)); Q8_0, Q6_K d * sum;
+// Q4_K (d sc) sum(q x) - (dmin m) sum(x); sum(x) per block or sub-block is
+// taken once per lane, x being the same for every row it streams.
+// Per 8 nibbles (Q4): 3 bit operations + 4 converts + 8 fma_mix.
 
 template <int DT>
 struct XFrag32 {
   float x[64];   // the item's x in the order item_dot forms its weight pairs
-  float sa, sb;  // Q4_K: sum of x over sub-block A (items 0..31) and B (32..63)
+  float sa, sb;  // Q4_0: sum of x over block 0 (elements 0..31) and block 1 (32..63);
+                 // Q4_K: over sub-block A (0..31) and B (32..63)
 };
 
 __device__ __forceinline__ half2_t h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ half2_t h2c(float c) { return half2_t{(_Float16)c, (_Float16)c}; }
+
+// The eight nibbles of a dword as exact fp16 pairs: pair 0 = low nibbles of
+// bytes 0, 1; pair 1 = bytes 2, 3; pairs 2, 3 the high nibbles.  A byte below
+// 16 read as OCP fp8 E4M3 is that integer times 2^-9 (the denormals run on
+// linearly into the first binade); the convert's scale operand contributes
+// its power of two, 2^9: 3 bit operations and 4 converts per 8 weights.
+__device__ __forceinline__ void nib4_f16(uint32_t w, half2_t (&E)[4]) {
+  const uint32_t l = w & 0x0F0F0F0Fu, h = (w >> 4) & 0x0F0F0F0Fu;
+  E[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l, 512.0f, false);
+  E[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(l, 512.0f, true);
+  E[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h, 512.0f, false);
+  E[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(h, 512.0f, true);
+}
+// Element (0..63 of the item) that half h of pair p of nibble dword t holds
+// in nib4_f16's order: byte 2 (p % 2) + h, low nibble for p < 2.
+template <int DT>
+__host__ __device__ constexpr int cvt_elem(int t, int p, int h) {
+  const int byte = 2 * (p & 1) + h, high = p >> 1;
+  if (DT == SWAMP_Q4_0) return 32 * (t / 4) + 8 * (t % 4) + 2 * byte + high;
+  return 32 * high + 4 * t + byte;  // Q4_K
+}
 
 // a += e.lo * x0, b += e.hi * x1 (two V_FMA_MIX_F32 with op_sel)
 __device__ __forceinline__ void fma2(half2_t e, float x0, float x1, float &a, float &b) {
@@ -381,17 +404,15 @@ __device__ __forceinline__ void build_xfrag(XFrag32<DT> &xf, const float4 (&x4)[
 #pragma unroll
       for (int p = 0; p < 4; p++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) xf.x[8 * t + 2 * p + h] = xv[nib_elem<DT>(t, p, h)];
-    if constexpr (DT == SWAMP_Q4_K) {
-      float sa = 0.f, sb = 0.f;
+        for (int h = 0; h < 2; h++) xf.x[8 * t + 2 * p + h] = xv[cvt_elem<DT>(t, p, h)];
+    float sa = 0.f, sb = 0.f;
 #pragma unroll
-      for (int i = 0; i < 32; i++) {
-        sa += xv[i];
-        sb += xv[32 + i];
-      }
-      xf.sa = sa;
-      xf.sb = sb;
+    for (int i = 0; i < 32; i++) {
+      sa += xv[i];
+      sb += xv[32 + i];
     }
+    xf.sa = sa;
+    xf.sb = sb;
   }
 }
 
@@ -401,16 +422,12 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag32<DT> &x
   if constexpr (DT == SWAMP_Q4_0) {
     const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
     const float d1 = swamp::f16_bits_to_f32(r.d[4] >> 16);
-    const half2_t lo_off = h2c(1032.f), hi_mul = h2c(0.0625f), hi_off = h2c(72.f);
     float s0a = 0.f, s0b = 0.f, s1a = 0.f, s1b = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) {
       const uint32_t w = t < 4 ? shr16(r.d[t + 1], r.d[t]) : r.d[t + 1];
-      uint32_t P[4];
-      nib_pairs(w, m, P);
-      // (1024 + q) - 1032 = q - 8;  (1024 + 16 q) / 16 - 72 = q - 8
-      const half2_t E[4] = {h2(P[0]) - lo_off, h2(P[1]) - lo_off, h2(P[2]) * hi_mul - hi_off,
-                            h2(P[3]) * hi_mul - hi_off};
+      half2_t E[4];
+      nib4_f16(w, E);  // the codes q, exact
       const float *x = xf.x + 8 * t;
 #pragma unroll
       for (int p = 0; p < 4; p++) {
@@ -418,7 +435,8 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag32<DT> &x
         else fma2(E[p], x[2 * p], x[2 * p + 1], s1a, s1b);
       }
     }
-    return d0 * (s0a + s0b) + d1 * (s1a + s1b);
+    // sum (q - 8) x = sum(q x) - 8 sum(x), per block; 8 sum(x) is exact
+    return d0 * ((s0a + s0b) - 8.0f * xf.sa) + d1 * ((s1a + s1b) - 8.0f * xf.sb);
   } else if constexpr (DT == SWAMP_Q8_0) {
     const float d0 = swamp::f16_bits_to_f32(r.d[0] & 0xFFFFu);
     const float d1 = swamp::f16_bits_to_f32(r.d[8] >> 16);
@@ -472,18 +490,16 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag32<DT> &x
     const float dmin = swamp::f16_bits_to_f32(r.h[0] >> 16);
     uint32_t sc0, m0, sc1, m1;
     q4k_scales(r.h, 2 * (item & 3), sc0, m0, sc1, m1);
-    // (1024 + q) - 1024 = q;  (1024 + 16 q) / 16 - 64 = q
-    const half2_t lo_off = h2c(1024.f), hi_mul = h2c(0.0625f), hi_off = h2c(64.f);
     float sa0 = 0.f, sa1 = 0.f, sb0 = 0.f, sb1 = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-      uint32_t P[4];
-      nib_pairs(r.q[t], m, P);
+      half2_t E[4];
+      nib4_f16(r.q[t], E);  // the codes q, exact: low nibbles sub-block A, high B
       const float *x = xf.x + 8 * t;
-      fma2(h2(P[0]) - lo_off, x[0], x[1], sa0, sa1);
-      fma2(h2(P[1]) - lo_off, x[2], x[3], sa0, sa1);
-      fma2(h2(P[2]) * hi_mul - hi_off, x[4], x[5], sb0, sb1);
-      fma2(h2(P[3]) * hi_mul - hi_off, x[6], x[7], sb0, sb1);
+      fma2(E[0], x[0], x[1], sa0, sa1);
+      fma2(E[1], x[2], x[3], sa0, sa1);
+      fma2(E[2], x[4], x[5], sb0, sb1);
+      fma2(E[3], x[6], x[7], sb0, sb1);
     }
     // sum ((d sc) q - dmin m) x = (d sc) sum(q x) - (dmin m) sum(x), per sub-block
     const float sv0 = d * float(sc0), mv0 = dmin * float(m0);

@@ -369,6 +369,21 @@ __host__ __device__ constexpr int cvt_elem(int t, int p, int h) {
   if (DT == SWAMP_Q4_0) return 32 * (t / 4) + 8 * (t % 4) + 2 * byte + high;
   return 32 * high + 4 * t + byte;  // Q4_K
 }
+// every element of the item exactly once
+template <int DT>
+constexpr bool cvt_elem_is_permutation() {
+  bool seen[64] = {};
+  for (int t = 0; t < 8; t++)
+    for (int p = 0; p < 4; p++)
+      for (int h = 0; h < 2; h++) {
+        const int e = cvt_elem<DT>(t, p, h);
+        if (e < 0 || e >= 64 || seen[e]) return false;
+        seen[e] = true;
+      }
+  return true;
+}
+static_assert(cvt_elem_is_permutation<SWAMP_Q4_0>(), "Q4_0 fp32-x element order");
+static_assert(cvt_elem_is_permutation<SWAMP_Q4_K>(), "Q4_K fp32-x element order");
 
 // a += e.lo * x0, b += e.hi * x1 (two V_FMA_MIX_F32 with op_sel)
 __device__ __forceinline__ void fma2(half2_t e, float x0, float x1, float &a, float &b) {

@@ -37,8 +37,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--cpu-threads 6,max] [--sweep] [--pmc-probe] [--pmc-gemm]
                        [--pmc-batched N]
 --sweep adds one JSON line per extra workload after the main line: the
-Q4_K small-batch sweep (1/4/8/16/17/24/32/64 tokens; more than 16 take the
-prefill-GEMM route) at 8B shapes and the 70B layer
+Q4_K small-batch sweep (1/4/8/16/17/24/32/64 tokens; 17-64 in token groups
+of 16) at 8B shapes and the 70B layer
 (decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
 --pmc-gemm the same for the 2048-token gate+up prefill GEMM; --pmc-batched N
@@ -278,8 +278,8 @@ SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 81
 
 def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
-    (lm_head Q8_0) for 1, 4, 8, 16 and 64 tokens (64: the entry point's
-    prefill-GEMM route), the 70B Q4_K layer as
+    (lm_head Q8_0) for 1, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
+    groups of 16), the 70B Q4_K layer as
     batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, and the 70B
     layer as a 4096-token bf16 prefill GEMM.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU

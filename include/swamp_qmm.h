@@ -179,13 +179,13 @@ SWAMP_API int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * fused_gemv_q4k_batched, fused_gemv_q4k.rs:527-554, :694).
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
- * 16 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass of one token
- * runs the decode GEMV, and n_tok > 16 runs swamp_qgemm's kernels on x
- * rounded to bf16 (in scratch; without scratch, passes of 16 instead).
- * Passes of 2..16 tokens round x to fp16 on the matrix cores (about 3e-5
- * of ||W_r|| ||x|| against the fp32 reference; more than 16 tokens, bf16:
- * about 1e-4): entries must lie within fp16 range (|x| < 65504), also for
- * accumulate = 1 and when no scratch is available.  Q6_K:
+ * pass of up to 64 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass
+ * of one token runs the decode GEMV, and n_tok > 64 runs swamp_qgemm's
+ * kernels on x rounded to bf16 (in scratch; without scratch, passes of 64
+ * instead).  Passes of 2..64 tokens round x to fp16 on the matrix cores
+ * (about 3e-5 of ||W_r|| ||x|| against the fp32 reference; more than 64
+ * tokens, bf16: about 1e-4): entries must lie within fp16 range
+ * (|x| < 65504), also for accumulate = 1 and when no scratch is available.  Q6_K:
  * forward_linear_batch sends it to fallback_gemv (linear.rs:336-364), the
  * GEMV per token written over y;
  * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
@@ -226,7 +226,7 @@ SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
 
 /* Scratch.  swamp_qgemv_batched and swamp_qgemm need scratch memory for
  * some shapes (the partial sums of K split across workgroups, and the bf16
- * copy of x of a batch of more than 16 tokens).  The library keeps one
+ * copy of x of a batch of more than 64 tokens).  The library keeps one
  * buffer per (device, stream) for it (hipStreamPerThread: per host thread
  * too), allocated on first use and replaced when a call needs more, both
  * stream-ordered on that stream (hipMallocAsync / hipFreeAsync): no call
@@ -234,7 +234,7 @@ SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
  * nothing is allocated: a call that needs more than the stream's buffer
  * holds takes the path without scratch (split pieces added with float
  * atomics into y cleared by a kernel, which is not bit-reproducible; more
- * than 16 tokens in passes of 16).  Calls on one stream must be issued from
+ * than 64 tokens in passes of 64).  Calls on one stream must be issued from
  * one host thread at a time: two threads calling on the same stream (the
  * null stream included) at once race on its buffer.
  *   swamp_qgemv_batched_workspace / swamp_qgemm_workspace: the scratch

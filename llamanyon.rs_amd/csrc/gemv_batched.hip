@@ -1,15 +1,17 @@
-// gemv_batched.hip -- small-batch (2..16 tokens per pass) quantized GEMV on
+// gemv_batched.hip -- small-batch (2..64 tokens per pass) quantized GEMV on
 // the matrix cores, for speculative verify and continuous batching.
 //
 // Replaces forward_linear_batch (swamp-engine/src/linear.rs:176-239) and
 // fused_gemv_q4k_batched (swamp-kernels/src/fused_gemv_q4k.rs:527-554,
 // scalar body :650-698).
 //
-// Still HBM-bound (at 16 tokens a Q4 weight byte feeds ~57 FLOP, the chip's
-// balance is ~300), so the weights must stream exactly once per pass of 16
-// tokens, with enough bytes in flight per CU to cover HBM latency.
+// Still HBM-bound (at 16 tokens a Q4 weight byte feeds ~57 FLOP, at 64
+// ~230, the chip's balance is ~300), so the weights must stream exactly once
+// per pass, with enough bytes in flight per CU to cover HBM latency.
 //  * V_MFMA_F32_16X16X32_F16 with A = activations (16 tokens x 32 k) and
-//    B = weights (32 k x 16 rows); C = 16 tokens x 16 rows, 4 VGPRs.
+//    B = weights (32 k x 16 rows); C = 16 tokens x 16 rows, 4 VGPRs.  Passes
+//    of 17..64 tokens run 2 or 4 token groups: every dequantized B fragment
+//    feeds one MFMA per group, each group with its own accumulators.
 //  * One workgroup of 16 waves per CU.  Its waves form Wt tile lanes x Wk
 //    K slices (Wt * Wk = 16): Wk = 1 for matrices with many tiles (each
 //    wave streams whole rows), up to 16 for the small ones, so that every
@@ -45,7 +47,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 16;      // waves per workgroup, one workgroup per CU
 constexpr int kThreads = kWaves * 64;
-constexpr int kTok = 16;        // tokens per pass (MFMA M)
+constexpr int kTok = 64;        // tokens per pass: up to 4 groups of 16 (MFMA M)
 constexpr int kRowsTile = 16;   // rows per tile (MFMA N)
 constexpr int kJmax = 2;        // tiles per wave whose accumulators stay in registers
 constexpr int kXLdsMax = 139264;             // activation bytes in LDS (one K phase)
@@ -311,6 +313,14 @@ __device__ __forceinline__ void lds_barrier() {
 // registers).
 template <int TOK>
 constexpr int frag_row() { return TOK + 1; }  // 16-byte slots per fragment row
+// Token groups of 16 a pass of TOK tokens runs per weight fragment (4, 8
+// and 16 tokens: one, with empty token rows below 16).
+template <int TOK>
+constexpr int token_groups() { return TOK > 16 ? TOK / 16 : 1; }
+template <int NG>
+struct Acc {
+  float4_t v[NG];
+};
 // r / n for r < 2^24, n > 0: the float quotient is within one of the
 // integer one, which one correction each way makes exact (no integer
 // division sequence, whose temporaries would hold registers while the
@@ -392,8 +402,11 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   const uint32_t chunk_bytes = kChunk * quad_bytes<DT>();
   float *slots = reinterpret_cast<float *>(xl + ipp * 8 * frag_row<TOK>());  // [16 waves][16 tok][16 rows]
 
-  auto tile_of = [&](int batch, int j) { return (b + (batch * kJmax + j) * G) * wt + tl; };
-  auto batch_len = [&](int batch) { return min(kJmax, J - batch * kJmax); };
+  // tiles per batch: one with four token groups (their accumulators take
+  // the registers of a second tile)
+  constexpr int kJ = token_groups<TOK>() > 2 ? 1 : kJmax;
+  auto tile_of = [&](int batch, int j) { return (b + (batch * kJ + j) * G) * wt + tl; };
+  auto batch_len = [&](int batch) { return min(kJ, J - batch * kJ); };
   auto advance = [&](Pos &q) {
     if (++q.c < cpw) return;
     q.c = 0;
@@ -446,45 +459,61 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   __syncthreads();
 
   // this lane's fragments: rows 8 * item + step of its items (item
-  // ks * ipw + g + 4 j), slot r16 % TOK
+  // ks * ipw + g + 4 j), slot r16 % TOK, plus 16 per token group
   constexpr int FR = frag_row<TOK>();
-  const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * FR + (r16 % TOK);
-  // accumulators of the batch's tiles (named registers: an indexed array
-  // would live in scratch, whose accesses share the vector memory counter
-  // with the weight prefetch and drain it)
-  float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  constexpr int NG = token_groups<TOK>();
+  const half8_t *xlane = xl + (ks * a.ipw + g) * 8 * FR + (TOK >= 16 ? r16 : r16 % TOK);
+  // accumulators of the batch's tiles, one 16x16 block per token group
+  // (registers: every index is a constant; an indexed array would live in
+  // scratch, whose accesses share the vector memory counter with the
+  // weight prefetch and drain it)
+  Acc<NG> acc0{}, acc1{};
   Pos qc{0, 0, 0, 0};  // chunk being consumed
 
   // Result of tile k of a batch: direct stores when a wave owns its tile's
   // whole K range, else a K-slice reduction through LDS.
-  auto emit_tile = [&](int batch, int k, const float4_t &v) {
+  auto emit_tile = [&](int batch, int k, const Acc<NG> &v) {
     const int tile = tile_of(batch, k);
     if (wk == 1) {
       if (tile < n_tiles) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) put_y(a, out, 4 * g + i, tile * kRowsTile + r16, v[i]);
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            put_y(a, out, 16 * gi + 4 * g + i, tile * kRowsTile + r16, v.v[gi][i]);
       }
       return;
     }
+    // K slices summed through LDS, one token group at a time (each group
+    // passed by a constant index: a loop over the groups around the
+    // barriers would index the accumulators at run time, in scratch)
     float *mine = slots + wave * 256;
+    auto reduce_group = [&](const float4_t &vg, int gi) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) mine[(4 * g + i) * 16 + r16] = v[i];
-    lds_barrier();
-    for (int o = tid; o < wt * 256; o += kThreads) {
-      const int otl = o >> 8, e = o & 255;
-      const float *src = slots + (otl << a.lwk) * 256 + e;
-      float sum = 0.f;
-      for (int s2 = 0; s2 < wk; s2++) sum += src[s2 * 256];
-      const int otile = (b + (batch * kJmax + k) * G) * wt + otl;
-      if (otile < n_tiles) put_y(a, out, e >> 4, otile * kRowsTile + (e & 15), sum);
+      for (int i = 0; i < 4; i++) mine[(4 * g + i) * 16 + r16] = vg[i];
+      lds_barrier();
+      for (int o = tid; o < wt * 256; o += kThreads) {
+        const int otl = o >> 8, e = o & 255;
+        const float *src = slots + (otl << a.lwk) * 256 + e;
+        float sum = 0.f;
+        for (int s2 = 0; s2 < wk; s2++) sum += src[s2 * 256];
+        const int otile = (b + (batch * kJ + k) * G) * wt + otl;
+        if (otile < n_tiles) put_y(a, out, 16 * gi + (e >> 4), otile * kRowsTile + (e & 15), sum);
+      }
+      lds_barrier();
+    };
+    reduce_group(v.v[0], 0);
+    if constexpr (NG > 1) reduce_group(v.v[1], 1);
+    if constexpr (NG > 2) {
+      reduce_group(v.v[2], 2);
+      reduce_group(v.v[3], 3);
     }
-    lds_barrier();
   };
   auto emit = [&](int batch) {
     const int jb = batch_len(batch);
     emit_tile(batch, 0, acc0);
     if (jb > 1) emit_tile(batch, 1, acc1);
-    acc0 = acc1 = float4_t{0.f, 0.f, 0.f, 0.f};
+    acc0 = acc1 = Acc<NG>{};
   };
 
   auto consume = [&](const Raw<DT> (&r)[kChunk]) {
@@ -494,16 +523,20 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       lds_barrier();
     }
     const half8_t *xc = xlane + qc.c * kChunk * 32 * FR;
-    float4_t c = acc0;
+    Acc<NG> c = acc0;
 #pragma unroll
     for (int i = 0; i < kChunk; i++) {
       Q4kScales kq{};
       if constexpr (DT == SWAMP_Q4_K) kq = q4k_item_scales(r[i], g);
 #pragma unroll
       for (int st = 0; st < 8; st++) {
-        const half8_t xa = xc[(i * 32 + st) * FR];
         const half8_t wb = weights_step<DT>(r[i], st, kq);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, c, 0, 0, 0);
+        // one dequantized B fragment feeds every token group
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+          const half8_t xa = xc[(i * 32 + st) * FR + 16 * gi];
+          c.v[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, wb, c.v[gi], 0, 0, 0);
+        }
       }
     }
     acc0 = c;
@@ -512,8 +545,11 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       // (selects, not branches: the optimizer turns the branchy form into a
       // store at a dynamic index, i.e. into scratch memory)
       const int jb = batch_len(qc.batch);
-      acc0 = jb > 1 ? acc1 : c;
-      acc1 = c;
+#pragma unroll
+      for (int gi = 0; gi < NG; gi++) {
+        acc0.v[gi] = jb > 1 ? acc1.v[gi] : c.v[gi];
+        acc1.v[gi] = c.v[gi];
+      }
       if (qc.j == jb - 1 && qc.p == P - 1) emit(qc.batch);
     }
     advance(qc);
@@ -649,9 +685,11 @@ int launch_pass_tok(Args a, hipStream_t s) {
     const KgPlan kp = kg_plan(a.n_tok, a.n_rows, a.n_cols, TOK);
     const int nkg = kp.nkg, q = kp.q;
     if (nkg > 1) {
-      if (q == 8)
-        return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, 0, nkg, s)
-                         : launch_geo<DT, TOK, 2, false>(a, 0, nkg, s);
+      if constexpr (token_groups<TOK>() == 1) {
+        if (q == 8)
+          return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, 0, nkg, s)
+                           : launch_geo<DT, TOK, 2, false>(a, 0, nkg, s);
+      }
       return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, 0, nkg, s)
                        : launch_geo<DT, TOK, 1, false>(a, 0, nkg, s);
     }
@@ -677,15 +715,21 @@ int launch_pass_tok(Args a, hipStream_t s) {
   // two-item chunks when that fits LDS and the row, else one-item chunks,
   // else fewer slices.
   while (best > 0 && ((4 << best) > xcap || (4 << best) > a.ipr)) best--;
-  if ((8 << best) <= xcap && (8 << best) <= a.ipr)
-    return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, 1, s)
-                     : launch_geo<DT, TOK, 2, false>(a, best, 1, s);
+  // token groups keep one-item chunks: their accumulators take the registers
+  // a second item would
+  if constexpr (token_groups<TOK>() == 1) {
+    if ((8 << best) <= xcap && (8 << best) <= a.ipr)
+      return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, 1, s)
+                       : launch_geo<DT, TOK, 2, false>(a, best, 1, s);
+  }
   return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, best, 1, s)
                    : launch_geo<DT, TOK, 1, false>(a, best, 1, s);
 }
 
 // Token count of the pass's activation layout (4, 8 or 16).
-int pass_tok(int n_tok) { return n_tok <= 4 ? 4 : n_tok <= 8 ? 8 : 16; }
+int pass_tok(int n_tok) {
+  return n_tok <= 4 ? 4 : n_tok <= 8 ? 8 : n_tok <= 16 ? 16 : n_tok <= 32 ? 32 : 64;
+}
 
 // K groups a pass of n_tok tokens will use (the plan launch_pass_tok follows).
 int pass_kgroups(int n_tok, int n_rows, int n_cols) {
@@ -696,14 +740,20 @@ template <int DT>
 int launch_pass(Args a, hipStream_t s) {
   if (a.n_tok <= 4) return launch_pass_tok<DT, 4>(a, s);
   if (a.n_tok <= 8) return launch_pass_tok<DT, 8>(a, s);
-  return launch_pass_tok<DT, 16>(a, s);
+  if (a.n_tok <= 16) return launch_pass_tok<DT, 16>(a, s);
+  if (a.n_tok <= 32) return launch_pass_tok<DT, 32>(a, s);
+  return launch_pass_tok<DT, 64>(a, s);
 }
 
 }  // namespace
 
 namespace {
 
-// The GEMM route of a call: more than 16 tokens written over y, on x rounded
+// Tokens per pass of the small-batch kernel: up to 64 (four token groups
+// per weight fragment).
+int pass_len(uint32_t) { return kTok; }
+
+// The GEMM route of a call: more than 64 tokens written over y, on x rounded
 // to bf16 (in scratch).
 bool gemm_route(int n_tok, int n_cols, int accumulate) {
   return n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
@@ -711,10 +761,11 @@ bool gemm_route(int n_tok, int n_cols, int accumulate) {
 }
 
 // Scratch of the small-batch passes: the largest K-group partial block.
-size_t kgroup_bytes(int n_tok, int n_rows, int n_cols, int accumulate) {
+size_t kgroup_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols, int accumulate) {
   size_t ws = 0;
-  for (int t0 = 0; t0 < n_tok; t0 += kTok) {
-    const int nt = std::min(kTok, n_tok - t0);
+  const int pl = pass_len(dtype);
+  for (int t0 = 0; t0 < n_tok; t0 += pl) {
+    const int nt = std::min(pl, n_tok - t0);
     if (nt == 1 && !accumulate) continue;  // the decode GEMV
     const int nkg = pass_kgroups(nt, n_rows, n_cols);
     if (nkg > 1) ws = std::max(ws, size_t(nkg) * nt * n_rows * sizeof(float));
@@ -733,7 +784,7 @@ size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_
     return xb + swamp_gemm_scratch_bytes(dtype, SWAMP_BF16, n_tok, n_rows, n_cols,
                                          limit > xb ? limit - xb : 0);
   }
-  return kgroup_bytes(n_tok, n_rows, n_cols, accumulate);
+  return kgroup_bytes(dtype, n_tok, n_rows, n_cols, accumulate);
 }
 
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
@@ -751,11 +802,9 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     }
     return SWAMP_OK;
   }
-  // Batches of more than 16 tokens written over y run as the prefill GEMM
-  // on x rounded to bf16 (in scratch): its 64-token tiles cost less than
-  // streaming the weights again per pass of 16 (8B Q4_0 gate+up at 24
-  // tokens: 36 us against 50 us; at 64: 42 us against 107 us).  Without
-  // scratch the passes below run instead.
+  // Batches of more than 64 tokens written over y run as the prefill GEMM
+  // on x rounded to bf16 (in scratch).  Without scratch the passes below
+  // run instead.
   if (gemm_route(n_tok, n_cols, accumulate)) {
     const size_t n = size_t(n_tok) * size_t(n_cols);
     if (void *xb = sc.get(n * 2)) {
@@ -777,11 +826,12 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return SWAMP_EDTYPE;
   // scratch for the passes that split K over workgroups; without it the
   // passes run as K phases
-  const size_t ws_bytes = kgroup_bytes(n_tok, n_rows, n_cols, accumulate);
+  const size_t ws_bytes = kgroup_bytes(dtype, n_tok, n_rows, n_cols, accumulate);
   a.ws = ws_bytes ? static_cast<float *>(sc.get(ws_bytes)) : nullptr;
   int rc = SWAMP_OK;
-  for (int t0 = 0; t0 < n_tok && rc == SWAMP_OK; t0 += kTok) {
-    a.n_tok = std::min(kTok, n_tok - t0);
+  const int pl = pass_len(dtype);
+  for (int t0 = 0; t0 < n_tok && rc == SWAMP_OK; t0 += pl) {
+    a.n_tok = std::min(pl, n_tok - t0);
     a.x = d_x + size_t(t0) * n_cols;
     a.y = d_y + size_t(t0) * n_rows;
     // a pass of one token written over y is a GEMV: the one-token kernel

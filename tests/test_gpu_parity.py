@@ -242,10 +242,12 @@ def test_gemv_multi(pkg, orc, torch_dev):
 # ------------------------------------------------------------ small batch
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
-@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19, 33, 70])
+@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19, 33, 64, 70])
 @pytest.mark.parametrize("rows,cols", [(1000, 4096), (256, 14336)])
-def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
-    # 1 token: the decode GEMV; 19, 33 and 70: the prefill GEMM on bf16-rounded x
+def test_batched_parity(pkg, orc, torch_dev, errlog, dtype, n_tok, rows, cols):
+    # 1 token: the decode GEMV; 2..64: the small-batch kernel (19 in two
+    # token groups of 16, 33 and 64 in four), x rounded to fp16; 70: the
+    # prefill GEMM on bf16-rounded x
     torch = torch_dev
     raw = weights(pkg, dtype, rows, cols, mid=n_tok)
     xs = acts(pkg, n_tok, cols, mid=n_tok)
@@ -258,7 +260,10 @@ def test_batched_parity(pkg, orc, torch_dev, dtype, n_tok, rows, cols):
     y = down(d_y)
     ref = orc.forward_linear_batch(dtype, raw, xs, rows, cols, 8)
     deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
-    assert orc.normalized_error(y, ref, deq, xs) <= TOL
+    err = orc.normalized_error(y, ref, deq, xs)
+    path = "gemv" if n_tok == 1 else "batched_f16" if n_tok <= 64 else "gemm_bf16"
+    errlog(f"batched {dtype} n_tok={n_tok} {rows}x{cols}", err, path=path)
+    assert err <= {"gemv": 1e-6, "batched_f16": 1e-4, "gemm_bf16": 4e-4}[path]
 
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
@@ -315,10 +320,11 @@ def test_batched_two_streams(pkg, torch_dev):
     kept per (device, stream): calls queued on two streams at once give the
     same bits as the same calls run one after another on one stream."""
     torch = torch_dev
-    # the last two run the GEMM route: bf16 x in one per-stream buffer, K
-    # pieces in the other
+    # 40 and 64 tokens: token groups with K groups; the last two run the
+    # GEMM route: bf16 x in one per-stream buffer, K pieces in the other
     cases = [(Q4_K, 16, 4096, 14336), (Q4_0, 8, 6144, 4096), (Q8_0, 12, 4096, 4096),
-             (Q4_0, 40, 4096, 4096), (Q4_K, 64, 6144, 4096)]
+             (Q4_0, 40, 4096, 4096), (Q4_K, 64, 6144, 4096), (Q4_0, 80, 4096, 4096),
+             (Q4_K, 96, 6144, 4096)]
     bufs = []
     for i, (dt, n_tok, rows, cols) in enumerate(cases):
         raw = weights(pkg, dt, rows, cols, mid=120 + i)
@@ -352,11 +358,11 @@ def test_batched_two_streams(pkg, torch_dev):
 
 
 @pytest.mark.parametrize("cols", [4096, 14336])
-@pytest.mark.parametrize("n_tok", [1, 6, 40])
+@pytest.mark.parametrize("n_tok", [1, 6, 40, 70])
 def test_batched_accumulate(pkg, orc, torch_dev, cols, n_tok):
     """accumulate=1 is the kernel contract of fused_gemv_q4k_batched
     (out += W x, fused_gemv_q4k.rs:694); it keeps every pass, of one token
-    or of more than 16, on the small-batch kernel."""
+    or of more than 64 (passes of 64), on the small-batch kernel."""
     torch = torch_dev
     rows = 512
     raw = weights(pkg, Q4_K, rows, cols, mid=3)

@@ -59,9 +59,11 @@ def test_workspace_queries(pkg, torch_dev):
     assert L.swamp_qgemm_workspace(Q4_0, BF16, 512, 28672, 4096) == 0
     # a long prompt: dequantize-once route (bf16 weight chunk + library workspace)
     assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 28672, 4096) > 0
-    # small batch: K groups on a short matrix; more than 16 tokens: bf16 x
+    # small batch: K groups on a short matrix (also with token groups, 40
+    # tokens); more than 64 tokens: bf16 x for the GEMM
     assert L.swamp_qgemv_batched_workspace(Q4_K, 16, 4096, 14336, 0) > 0
-    assert L.swamp_qgemv_batched_workspace(Q4_0, 40, 4096, 4096, 0) >= 40 * 4096 * 2
+    assert L.swamp_qgemv_batched_workspace(Q4_0, 40, 4096, 4096, 0) > 0
+    assert L.swamp_qgemv_batched_workspace(Q4_0, 80, 4096, 4096, 0) >= 80 * 4096 * 2
     assert L.swamp_qgemv_batched_workspace(Q4_K, 1, 4096, 14336, 0) == 0
     assert L.swamp_workspace_reserve(None, 0) == 0
 
@@ -129,11 +131,13 @@ def test_gemm_small_m_single_piece(pkg, orc, torch_dev, errlog, dtype, m, rows, 
 
 
 def _calls(pkg, torch, mid):
-    """Calls that take scratch: small batch with K groups, small batch of
-    40 tokens (bf16 x + GEMM pieces), GEMM split into pieces."""
+    """Calls that take scratch: small batch with K groups (16 tokens, and
+    40 in token groups), small batch of 80 tokens (bf16 x + GEMM pieces),
+    GEMM split into pieces."""
     out = []
     for kind, dtype, n, rows, cols in [("batched", Q4_K, 16, 4096, 14336),
-                                       ("batched", Q4_0, 40, 1024, 4096),
+                                       ("batched", Q4_K, 40, 1024, 4096),
+                                       ("batched", Q4_0, 80, 1024, 4096),
                                        ("gemm", Q8_0, 64, 512, 4096)]:
         raw = weights(pkg, dtype, rows, cols, mid=mid ^ rows)
         x = acts(pkg, n, cols, mid=mid ^ rows)
@@ -199,8 +203,8 @@ def test_graph_capture_with_reserved_scratch(pkg, torch_dev):
 def test_graph_capture_without_scratch(pkg, orc, torch_dev, errlog):
     """A fresh stream captured without a reservation allocates nothing: the
     calls take the path without scratch (K pieces and K groups added with
-    float atomics into y cleared by a kernel; more than 16 tokens in passes
-    of 16), which stays within the contract on every replay."""
+    float atomics into y cleared by a kernel; more than 64 tokens in passes
+    of 64), which stays within the contract on every replay."""
     torch = torch_dev
     cs = torch.cuda.Stream()
     calls = _calls(pkg, torch, mid=2)

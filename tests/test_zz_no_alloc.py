@@ -35,9 +35,9 @@ def test_noalloc_matches_batched_two_calls(pkg, orc, torch_dev, errlog):
     torch = torch_dev
     L = pkg.gpu_lib()
     s = torch.cuda.current_stream().cuda_stream
-    # first call: 40 tokens (bf16 x and K pieces in scratch); second, a
+    # first call: 80 tokens (bf16 x and K pieces in scratch); second, a
     # smaller input: 8 tokens on a short matrix (K groups in scratch)
-    cases = [(Q4_0, 40, 4096, 4096, 1, False), (Q4_K, 8, 1024, 14336, 2, False),
+    cases = [(Q4_0, 80, 4096, 4096, 1, False), (Q4_K, 8, 1024, 14336, 2, False),
              (Q8_0, 16, 4096, 4096, 3, True)]
     for dtype, n_tok, rows, cols, mid, acc in cases:
         need = L.swamp_qgemv_batched_workspace(dtype, n_tok, rows, cols, int(acc))

@@ -280,8 +280,9 @@ def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
     (lm_head Q8_0) for 1, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
     groups of 16), the 70B Q4_K layer as
-    batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, and the 70B
-    layer as a 4096-token bf16 prefill GEMM.  Each matrix is
+    batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, the 70B
+    layer as a 4096-token bf16 prefill GEMM, and the 8B layer (without
+    lm_head) as a 2048-token int8 GEMM with Q4_K and Q4_0 weights.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU
     sleep; GB/s over the algorithmic bytes, TFLOP/s over 2*M*rows*K."""
     s = stream.cuda_stream
@@ -412,6 +413,32 @@ def run_sweep(pkg, torch, np, stream, lib):
         del ws, xb, y
     print(json.dumps({"sweep": "llama3-70b prefill Q4_K (lm_head Q8_0) x bf16, 4096 tokens",
                       "matrices": per}),
+          flush=True)
+    # 8B prefill, 2048 tokens, Q4_K weights on the int8 MFMA against Q8_0 x
+    # (quantizer included), beside the same calls with Q4_0 weights
+    m = 2048
+    per = []
+    for i, (name, rows, k) in enumerate(SWEEP_8B[:4]):
+        x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x700 ^ i, 1.0, m, k)).cuda()
+        xq = torch.empty(m * k // 32 * 34, dtype=torch.uint8, device="cuda")
+        y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+        for dt in (pkg.Q4_K, pkg.Q4_0):
+            ws = weights_dev(dt, rows, k, SEED ^ 0x800 ^ i, 0.02, 1)
+
+            def fn(c, dt=dt, ws=ws, rows=rows, k=k, x=x, xq=xq, y=y):
+                check(lib.swamp_quantize_q8_0(x.data_ptr(), pkg.F32, xq.data_ptr(), m * k, s),
+                      "swamp_quantize_q8_0")
+                check(lib.swamp_qgemm(dt, ws[0].data_ptr(), ws[0].numel(), xq.data_ptr(),
+                                      pkg.Q8_0, y.data_ptr(), m, rows, k, s), "swamp_qgemm int8")
+            us = timed(fn, reps=10)
+            tops = 2 * m * rows * k / us / 1e6
+            per.append({"name": name, "dtype": pkg.DTYPE_NAMES[dt], "rows": rows, "k": k,
+                        "us": round(us, 1), "TOP/s": round(tops, 1),
+                        "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)})
+            del ws
+        del x, xq, y
+    print(json.dumps({"sweep": "llama3-8b prefill int8 MFMA x Q8_0 (quantizer included), "
+                               "Q4_K and Q4_0 weights, 2048 tokens", "matrices": per}),
           flush=True)
 
 

@@ -202,11 +202,13 @@ SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     registers to bf16 and fed to bf16 MFMA (fp32 accumulate).
  *   x_type SWAMP_Q8_0: d_x is Q8_0 blocks [m][n_cols/32] (as produced by
  *     swamp_quantize_q8_0); int8 MFMA (one 32x32x32 instruction per
- *     32-weight block) against W's int8 codes (Q4_0: nibble - 8), each
- *     block's int32 result scaled by d_w * d_x into fp32.  Q4_0 and Q8_0
- *     weights only; n_cols a multiple of 128.
- * dtype Q4_0, Q8_0, Q4_K or Q6_K (Q4_K and Q6_K with bf16 x only); bf16 x
- * needs n_cols a multiple of 64.
+ *     32-weight block) against W's int8 codes (Q4_0: nibble - 8; Q4_K:
+ *     the nibble, with d * sc as the block scale and dmin * m * d_x *
+ *     sum(q_x) subtracted per block), each block's int32 result scaled by
+ *     d_w * d_x into fp32.  Q4_0, Q8_0 and Q4_K weights; n_cols a multiple
+ *     of 128.
+ * dtype Q4_0, Q8_0, Q4_K or Q6_K (Q6_K with bf16 x only); bf16 x needs
+ * n_cols a multiple of 64.
  * Below 1024 tokens (bf16 x) the fused kernel dequantizes weight tiles in
  * registers to bf16; when the tiles do not fill the GPU, K is split across
  * workgroups whose partial tiles go to scratch and are summed in piece

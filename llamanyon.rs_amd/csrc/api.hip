@@ -387,7 +387,7 @@ int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len, const void *d_x, 
   if (int rc = check_gemv_args(dtype, d_w, w_len, n_rows, n_cols)) return rc;
   if (m < 0) return SWAMP_EINVAL;
   if (x_type != SWAMP_BF16 && x_type != SWAMP_Q8_0) return SWAMP_EDTYPE;
-  if (x_type == SWAMP_Q8_0 && (dtype == SWAMP_Q4_K || dtype == SWAMP_Q6_K)) return SWAMP_EDTYPE;
+  if (x_type == SWAMP_Q8_0 && dtype == SWAMP_Q6_K) return SWAMP_EDTYPE;
   if (m == 0 || n_rows == 0) return SWAMP_OK;
   if (!d_x || !d_y || !aligned(d_x, 16) || !aligned(d_y, 4)) return SWAMP_EINVAL;
   if (n_cols % (x_type == SWAMP_Q8_0 ? 128 : 64) != 0) return SWAMP_ESHAPE;

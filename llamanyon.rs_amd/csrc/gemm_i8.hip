@@ -1,6 +1,9 @@
 // gemm_i8.hip -- prefill GEMM with int8 matrix cores against Q8_0-quantized
 // activations: y[m][r] = sum_b d_w[r,b] d_x[m,b] sum_{i in b} qw[r,i] qx[m,i]
-// for Q4_0 (qw = nibble - 8) or Q8_0 (qw = int8) weights.
+// for Q4_0 (qw = nibble - 8) or Q8_0 (qw = int8) weights.  Q4_K weights
+// (W = d sc q - dmin m per 32-weight sub-block, q4_k.rs:278-321) take
+// qw = q (0..15), d_w = d sc, and subtract dmin m d_x sum_{i in b} qx[m,i]
+// per block: the same dot, regrouped.
 //
 // Replaces, like gemm.hip, the prefill use of forward_linear_batch
 // (swamp-engine/src/executor.rs:106-110 -> linear.rs:176-239), with the
@@ -15,7 +18,7 @@
 //    plus per-block fp32 scales; two LDS stages, one barrier per step.
 //  * Each block's int32 32 x 32 result is converted and added into the
 //    fp32 accumulators with its two scales: three vector ops per output
-//    element per block.  With a scale per 32-block on both sides this
+//    element per block (Q4_K four: the minimum term is one more FMA).  With a scale per 32-block on both sides this
 //    per-element work, not the matrix cores, bounds the kernel (the 32-deep
 //    int8 MFMA does 32 MACs per element in the time the vector ALU does
 //    about five element ops).
@@ -27,6 +30,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace {
 
@@ -45,8 +49,17 @@ constexpr int kThreads = 256;
 // activation scales [4][128] f32, weight scales [4][128] f32.
 constexpr int kQBytes = kBM * kBlk * 32;  // 16 KB
 constexpr int kSBytes = kBlk * kBM * 4;   // 2 KB
-constexpr int kStageBytes = 2 * kQBytes + 2 * kSBytes;
-constexpr int kSmemBytes = 2 * kStageBytes;  // 72 KB
+// Q4_K adds two scale arrays: the weight minimums dmin * m [4][128] and
+// the activation block sums d_x * sum(qx) [4][128].
+template <int DT>
+constexpr int stage_bytes() {
+  return 2 * kQBytes + (DT == SWAMP_Q4_K ? 4 : 2) * kSBytes;
+}
+template <int DT>
+constexpr int smem_bytes() {  // 72 KB, Q4_K 80 KB (two workgroups per CU)
+  return 2 * stage_bytes<DT>();
+}
+static_assert(2 * smem_bytes<SWAMP_Q4_K>() <= 160 * 1024, "two Q4_K workgroups per CU");
 
 // 16-byte chunk `chunk` (0..7) of quant row `row`, XOR-swizzled by row
 // pairs (the 16-row groups of a fragment read hit 16 distinct bank quads).
@@ -73,7 +86,8 @@ struct Geo {
 };
 
 // Raw bytes of step kt for this thread: two activation Q8_0 blocks (68 B)
-// and two weight blocks (one Q4_0 item of 36 B or two Q8_0 blocks of 68 B).
+// and two weight blocks (one Q4_0 item of 36 B, two Q8_0 blocks of 68 B,
+// or a Q4_K quarter: the super-block's 16-byte header and 32 nibble bytes).
 template <int DT>
 struct Stage {
   Raw<SWAMP_Q8_0> x;
@@ -101,15 +115,27 @@ __device__ __forceinline__ void sload(Stage<DT> &st, const Geo &g, int kt) {
 #pragma unroll
     for (int i = 0; i < 4; i++) { st.w.d[i] = a[i]; st.w.d[4 + i] = b[i]; }
     st.w.d[8] = __builtin_amdgcn_raw_buffer_load_b32(g.wr, g.wv + 32, s, 0);
+  } else if constexpr (DT == SWAMP_Q4_K) {
+    // item 2 kt + half = quarter 2 (kt & 1) + half of super-block kt / 2:
+    // its 16-byte header and 32 nibble bytes (g.wv = row start + 16 + 32 half)
+    const uint32_t sb = uint32_t(kt >> 1) * 144u;
+    const u32x4v_t h = __builtin_amdgcn_raw_buffer_load_b128(g.wr, g.wv - 16u - 32u * uint32_t(g.half),
+                                                             sb, 0);
+    const uint32_t sq = sb + 64u * uint32_t(kt & 1);
+    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(g.wr, g.wv, sq, 0);
+    const u32x4v_t b = __builtin_amdgcn_raw_buffer_load_b128(g.wr, g.wv + 16, sq, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) { st.w.h[i] = h[i]; st.w.q[i] = a[i]; st.w.q[4 + i] = b[i]; }
   } else {
     load_q8_pair(st.w, g.wr, g.wv, uint32_t(kt) * 136u);
   }
 }
 
 // Two Q8_0 blocks (17 dwords, block 0's quants start at byte 2) -> two
-// quant chunks of 32 B each and two scales.
+// quant chunks of 32 B each and two scales; with `sums`, also each block's
+// d * sum(q) (exact: |sum| <= 4096 times an fp16 fits fp32's 24 bits).
 __device__ __forceinline__ void unpack_q8_pair(const Raw<SWAMP_Q8_0> &r, uint8_t *q, float *s,
-                                               const Geo &g) {
+                                               float *sums, const Geo &g) {
 #pragma unroll
   for (int b = 0; b < 2; b++) {
     uint32_t v[8];
@@ -118,17 +144,49 @@ __device__ __forceinline__ void unpack_q8_pair(const Raw<SWAMP_Q8_0> &r, uint8_t
     const int blk = 2 * g.half + b;
     *reinterpret_cast<u32x4v_t *>(q + qswz(g.row, 2 * blk)) = u32x4v_t{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<u32x4v_t *>(q + qswz(g.row, 2 * blk + 1)) = u32x4v_t{v[4], v[5], v[6], v[7]};
-    s[blk * kBM + g.row] = swamp::f16_bits_to_f32(b == 0 ? (r.d[0] & 0xFFFFu) : (r.d[8] >> 16));
+    const float d = swamp::f16_bits_to_f32(b == 0 ? (r.d[0] & 0xFFFFu) : (r.d[8] >> 16));
+    s[blk * kBM + g.row] = d;
+    if (sums) {
+      int sum = 0;
+#pragma unroll
+      for (int t = 0; t < 8; t++) sum = __builtin_amdgcn_sdot4(int(v[t]), 0x01010101, sum, false);
+      sums[blk * kBM + g.row] = d * float(sum);
+    }
   }
 }
 
 template <int DT>
-__device__ __forceinline__ void lstore(uint8_t *stg, const Stage<DT> &st, const Geo &g) {
+__device__ __forceinline__ void lstore(uint8_t *stg, const Stage<DT> &st, const Geo &g, int kt) {
   uint8_t *xq = stg, *wq = stg + kQBytes;
   float *xs = reinterpret_cast<float *>(stg + 2 * kQBytes);
   float *wsc = xs + kBlk * kBM;
-  unpack_q8_pair(st.x, xq, xs, g);
-  if constexpr (DT == SWAMP_Q4_0) {
+  float *wmn = wsc + kBlk * kBM, *xsum = wmn + kBlk * kBM;  // Q4_K only
+  unpack_q8_pair(st.x, xq, xs, DT == SWAMP_Q4_K ? xsum : nullptr, g);
+  if constexpr (DT == SWAMP_Q4_K) {
+    // quarter 2 (kt & 1) + half: sub-block 2 quarter (low nibbles, block
+    // 2 half of the step) and 2 quarter + 1 (high nibbles, block 2 half + 1)
+    const int quarter = 2 * (kt & 1) + g.half;
+    uint32_t sc0, m0, sc1, m1;
+    swamp::q4k_scales(st.w.h, 2 * quarter, sc0, m0, sc1, m1);
+    const float d = swamp::f16_bits_to_f32(st.w.h[0] & 0xFFFFu);
+    const float dmin = swamp::f16_bits_to_f32(st.w.h[0] >> 16);
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      lo[t] = st.w.q[t] & 0x0F0F0F0Fu;
+      hi[t] = (st.w.q[t] >> 4) & 0x0F0F0F0Fu;
+    }
+    const int b0 = 2 * g.half, b1 = b0 + 1;
+    *reinterpret_cast<u32x4v_t *>(wq + qswz(g.row, 2 * b0)) = u32x4v_t{lo[0], lo[1], lo[2], lo[3]};
+    *reinterpret_cast<u32x4v_t *>(wq + qswz(g.row, 2 * b0 + 1)) = u32x4v_t{lo[4], lo[5], lo[6], lo[7]};
+    *reinterpret_cast<u32x4v_t *>(wq + qswz(g.row, 2 * b1)) = u32x4v_t{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4v_t *>(wq + qswz(g.row, 2 * b1 + 1)) = u32x4v_t{hi[4], hi[5], hi[6], hi[7]};
+    // exact products (an fp16 times a 6-bit code), as the dequantizer forms them
+    wsc[b0 * kBM + g.row] = d * float(sc0);
+    wsc[b1 * kBM + g.row] = d * float(sc1);
+    wmn[b0 * kBM + g.row] = dmin * float(m0);
+    wmn[b1 * kBM + g.row] = dmin * float(m1);
+  } else if constexpr (DT == SWAMP_Q4_0) {
 #pragma unroll
     for (int b = 0; b < 2; b++) {
       uint32_t v[8];
@@ -145,24 +203,26 @@ __device__ __forceinline__ void lstore(uint8_t *stg, const Stage<DT> &st, const 
           swamp::f16_bits_to_f32(b == 0 ? (st.w.d[0] & 0xFFFFu) : (st.w.d[4] >> 16));
     }
   } else {
-    unpack_q8_pair(st.w, wq, wsc, g);
+    unpack_q8_pair(st.w, wq, wsc, nullptr, g);
   }
 }
 
 // One K step (four blocks) on LDS stage `stg`.
+template <int DT>
 __device__ __forceinline__ void compute(f32x16_t (&acc)[2][2], const uint8_t *stg, int wm, int wn,
                                         int lane) {
   const uint8_t *xq = stg, *wq = stg + kQBytes;
   const float *xs = reinterpret_cast<const float *>(stg + 2 * kQBytes);
   const float *wsc = xs + kBlk * kBM;
+  const float *wmn = wsc + kBlk * kBM, *xsum = wmn + kBlk * kBM;  // Q4_K only
   const int fr = lane & 31, fc = lane >> 5;
   // one block per trip, not unrolled: the sixteen int32 tiles of four
   // unrolled blocks would all be live at once
 #pragma unroll 1
   for (int blk = 0; blk < kBlk; blk++) {
     i32x4_t a[2], b[2];
-    float dw[2];
-    f32x4_t dx[2][4];
+    float dw[2], mw[2];
+    f32x4_t dx[2][4], sx[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int r = wm * 64 + i * 32;
@@ -170,14 +230,18 @@ __device__ __forceinline__ void compute(f32x16_t (&acc)[2][2], const uint8_t *st
       // activation scales of the 16 rows this lane's outputs cover:
       // rows r + 8q + 4 fc + (0..3), q = 0..3
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+      for (int q = 0; q < 4; q++) {
         dx[i][q] = *reinterpret_cast<const f32x4_t *>(xs + blk * kBM + r + 8 * q + 4 * fc);
+        if constexpr (DT == SWAMP_Q4_K)
+          sx[i][q] = *reinterpret_cast<const f32x4_t *>(xsum + blk * kBM + r + 8 * q + 4 * fc);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int r = wn * 64 + j * 32 + fr;
       b[j] = *reinterpret_cast<const i32x4_t *>(wq + qswz(r, 2 * blk + fc));
       dw[j] = wsc[blk * kBM + r];
+      if constexpr (DT == SWAMP_Q4_K) mw[j] = -wmn[blk * kBM + r];
     }
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -186,8 +250,11 @@ __device__ __forceinline__ void compute(f32x16_t (&acc)[2][2], const uint8_t *st
         const i32x16_t zero = {};
         const i32x16_t c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], zero, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 16; e++)
-          acc[i][j][e] = __builtin_fmaf(float(c[e]), dx[i][e >> 2][e & 3] * dw[j], acc[i][j][e]);
+        for (int e = 0; e < 16; e++) {
+          float t = __builtin_fmaf(float(c[e]), dx[i][e >> 2][e & 3] * dw[j], acc[i][j][e]);
+          if constexpr (DT == SWAMP_Q4_K) t = __builtin_fmaf(mw[j], sx[i][e >> 2][e & 3], t);
+          acc[i][j][e] = t;
+        }
       }
   }
 }
@@ -222,7 +289,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
   g.xr = swamp::make_rsrc(xq8 + size_t(m0) * xrow, uint32_t(size_t(mrows) * xrow));
   g.xv = uint32_t(size_t(g.row) * xrow + 68u * uint32_t(g.half));
   g.wr = swamp::make_rsrc(w + size_t(n0) * row_bytes, uint32_t(size_t(nrows) * row_bytes));
-  g.wv = uint32_t(size_t(g.row) * row_bytes + (DT == SWAMP_Q4_0 ? 36u : 68u) * uint32_t(g.half));
+  g.wv = uint32_t(size_t(g.row) * row_bytes +
+                  (DT == SWAMP_Q4_0 ? 36u : DT == SWAMP_Q8_0 ? 68u : 32u) * uint32_t(g.half) +
+                  (DT == SWAMP_Q4_K ? 16u : 0u));
 
   f32x16_t acc[2][2];
 #pragma unroll
@@ -234,16 +303,16 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
 
   Stage<DT> st;
   sload<DT>(st, g, kt0);
-  lstore<DT>(smem, st, g);
+  lstore<DT>(smem, st, g, kt0);
   __syncthreads();
   for (int kt = kt0; kt < kt1; kt++) {
     const int s = (kt - kt0) & 1;
-    const uint8_t *cur = smem + s * kStageBytes;
-    uint8_t *nxt = smem + (s ^ 1) * kStageBytes;
+    const uint8_t *cur = smem + s * stage_bytes<DT>();
+    uint8_t *nxt = smem + (s ^ 1) * stage_bytes<DT>();
     const bool more = kt + 1 < kt1;
     if (more) sload<DT>(st, g, kt + 1);
-    compute(acc, cur, wm, wn, lane);
-    if (more) lstore<DT>(nxt, st, g);
+    compute<DT>(acc, cur, wm, wn, lane);
+    if (more) lstore<DT>(nxt, st, g, kt + 1);
     __syncthreads();
   }
 
@@ -277,7 +346,7 @@ int set_smem_attr_i8() {
   static hipError_t err = hipSuccess;
   std::call_once(once, [] {
     err = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_i8_kernel<DT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, smem_bytes<DT>());
   });
   return err == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }
@@ -301,7 +370,7 @@ void plan_i8(int m, int n_rows, int n_cols, int &splits, int &kt_per_split) {
 
 size_t swamp_gemm_i8_scratch_bytes(uint32_t dtype, int m, int n_rows, int n_cols) {
   if (m <= 0 || n_rows <= 0 || n_cols % (32 * kBlk) != 0) return 0;
-  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0) return 0;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return 0;
   int splits, kps;
   plan_i8(m, n_rows, n_cols, splits, kps);
   return splits > 1 ? size_t(splits) * size_t(m) * size_t(n_rows) * sizeof(float) : 0;
@@ -310,7 +379,7 @@ size_t swamp_gemm_i8_scratch_bytes(uint32_t dtype, int m, int n_rows, int n_cols
 int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, float *d_y, int m,
                          int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s) {
   if (m == 0 || n_rows == 0) return SWAMP_OK;
-  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0) return SWAMP_EDTYPE;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return SWAMP_EDTYPE;
   if (n_cols % (32 * kBlk) != 0) return SWAMP_ESHAPE;
   const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n_rows + kBN - 1) / kBN;
   const int tiles = tiles_m * tiles_n;
@@ -330,15 +399,17 @@ int swamp_launch_gemm_i8(uint32_t dtype, const void *d_w, const void *d_xq8, flo
   const uint8_t *w = static_cast<const uint8_t *>(d_w);
   const uint8_t *x = static_cast<const uint8_t *>(d_xq8);
   const size_t rb = swamp::row_bytes(int(dtype), size_t(n_cols));
-  if (dtype == SWAMP_Q4_0) {
-    if (int rc = set_smem_attr_i8<SWAMP_Q4_0>()) return rc;
-    gemm_i8_kernel<SWAMP_Q4_0><<<grid, kThreads, kSmemBytes, s>>>(
+  auto launch = [&](auto dt) -> int {
+    constexpr int DT = decltype(dt)::value;
+    if (int rc = set_smem_attr_i8<DT>()) return rc;
+    gemm_i8_kernel<DT><<<grid, kThreads, smem_bytes<DT>(), s>>>(
         w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic, part);
-  } else {
-    if (int rc = set_smem_attr_i8<SWAMP_Q8_0>()) return rc;
-    gemm_i8_kernel<SWAMP_Q8_0><<<grid, kThreads, kSmemBytes, s>>>(
-        w, x, d_y, m, n_rows, n_cols, rb, tiles_m, tiles_n, kt_per_split, atomic, part);
-  }
+    return SWAMP_OK;
+  };
+  int rc = dtype == SWAMP_Q4_0   ? launch(std::integral_constant<int, SWAMP_Q4_0>{})
+           : dtype == SWAMP_Q8_0 ? launch(std::integral_constant<int, SWAMP_Q8_0>{})
+                                 : launch(std::integral_constant<int, SWAMP_Q4_K>{});
+  if (rc) return rc;
   if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;
   if (part) return swamp_launch_split_reduce(part, d_y, splits, n, s);
   return SWAMP_OK;

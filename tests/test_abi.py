@@ -104,7 +104,6 @@ def test_argument_validation_precedes_device(pkg):
     assert L.swamp_qgemv(pkg.Q4_K, fake + 4, 1 << 20, fake, fake, 4, 256, None) == pkg.EINVAL
     assert L.swamp_qgemv(pkg.Q4_0, fake, 1 << 20, fake + 4, fake, 4, 64, None) == pkg.EINVAL
     assert L.swamp_qgemv_batched(pkg.Q4_0, fake, 1 << 20, fake, fake, -1, 4, 64, 0, None) == pkg.EINVAL
-    assert L.swamp_qgemm(pkg.Q4_K, fake, 1 << 20, fake, pkg.Q8_0, fake, 4, 4, 256, None) == pkg.EDTYPE
     assert L.swamp_qgemm(pkg.Q4_0, fake, 1 << 20, fake, pkg.F16, fake, 4, 4, 64, None) == pkg.EDTYPE
     assert L.swamp_qdequant(13, fake, 1 << 20, fake, 64, None) == pkg.EDTYPE
     # Q6_K: whole 256-blocks, 4-byte aligned rows base, enough bytes; no

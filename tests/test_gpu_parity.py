@@ -467,14 +467,17 @@ def test_gemm_rows_tail_and_token_consistency(pkg, orc, torch_dev):
     assert orc.normalized_error(y[m - 1], g, deq, x_fed[m - 1]) <= 2 * TOL
 
 
-@pytest.mark.parametrize("dtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
 @pytest.mark.parametrize("m,rows,cols", [(512, 4096, 4096), (77, 300, 1024), (2048, 512, 4096),
-                                         (256, 1024, 14336), (1, 33, 128)])
+                                         (256, 1024, 14336), (1, 33, 128), (130, 200, 768)])
 def test_gemm_int8_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
     """int8 matrix-core GEMM against Q8_0 activations: x is quantized on the
     device (swamp_quantize_q8_0, byte-identical to the host quantizer), and
     the oracle multiplies the dequantized Q8_0 activations -- the values the
-    kernel actually consumed."""
+    kernel actually consumed.  Q4_K rows are whole 256-weight super-blocks;
+    768 columns are 6 K steps of 128, three super-blocks."""
+    if dtype == Q4_K and cols % 256:
+        pytest.skip("Q4_K rows are whole 256-weight super-blocks")
     torch = torch_dev
     raw = weights(pkg, dtype, rows, cols, mid=m + 5)
     x = acts(pkg, m, cols, mid=m + 5)
@@ -508,11 +511,11 @@ def test_gemm_int8_argument_errors(pkg, torch_dev):
         pkg.qgemm(Q4_0, d_w.data_ptr(), raw.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m, rows,
                   cols, stream(torch))
     assert e.value.code == pkg.ESHAPE
-    rawk = weights(pkg, Q4_K, rows, 256)
+    rawk = weights(pkg, pkg.Q6_K, rows, 512)
     d_wk = up(torch, rawk)
     with pytest.raises(pkg.GpuError) as e:
-        pkg.qgemm(Q4_K, d_wk.data_ptr(), rawk.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m,
-                  rows, 256, stream(torch))
+        pkg.qgemm(pkg.Q6_K, d_wk.data_ptr(), rawk.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m,
+                  rows, 512, stream(torch))
     assert e.value.code == pkg.EDTYPE
     torch.cuda.synchronize()
     assert np.all(down(d_y) == 0)  # nothing written on error

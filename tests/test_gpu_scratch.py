@@ -68,7 +68,7 @@ def test_workspace_queries(pkg, torch_dev):
     assert L.swamp_workspace_reserve(None, 0) == 0
 
 
-@pytest.mark.parametrize("dtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
 def test_gemm_int8_split_repeat_bitwise(pkg, orc, torch_dev, errlog, dtype):
     """The int8 GEMM's K pieces are summed in piece order: repeated calls,
     with other shapes in between, give identical bits."""

@@ -24,7 +24,7 @@ TOL = 1e-3
 # Per-path bounds, each a few times the error the path's rounding of its
 # operands gives on these N(0, 1) activations and N(0, sigma) weights:
 #   GEMV, fp32 x and fp32 sums (the reference's arithmetic): summation order only;
-#   small batch (2..16 tokens), x rounded to fp16 (2^-11 relative);
+#   small batch (2..64 tokens), x rounded to fp16 (2^-11 relative);
 #   GEMM, x and the dequantized weights rounded to bf16 (2^-8 relative each);
 #   int8 GEMM, x quantized to Q8_0 (the oracle multiplies the same Q8_0 x).
 BOUND = {"gemv": 1e-6, "batched_f16": 1e-4, "gemm_bf16": 4e-4, "gemm_i8": 1e-5}

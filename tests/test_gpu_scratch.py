@@ -273,7 +273,7 @@ def test_per_thread_default_stream(pkg, torch_dev):
 
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_batched_large_activation_within_fp16_range(pkg, orc, torch_dev, errlog, accumulate):
-    """The 2..16-token passes round x to fp16: an activation of 6e4 (inside
+    """The 2..64-token passes round x to fp16: an activation of 6e4 (inside
     fp16 range, documented limit |x| < 65504) still gives results within
     the contract, also on the accumulating form."""
     torch = torch_dev

@@ -280,7 +280,7 @@ def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
     (lm_head Q8_0) for 1, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
     groups of 16), the 70B Q4_K layer as
-    batch-1 decode, the 8B shapes in Q6_K as batch-1 decode, the 70B
+    batch-1 decode, the 8B shapes in Q6_K at 1, 4, 16 and 32 tokens, the 70B
     layer as a 4096-token bf16 prefill GEMM, and the 8B layer (without
     lm_head) as a 2048-token int8 GEMM with Q4_K and Q4_0 weights.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU
@@ -341,28 +341,37 @@ def run_sweep(pkg, torch, np, stream, lib):
                               "GB/s": round(tot_b / tot_us / 1e3, 1),
                               "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
                               "matrices": per}), flush=True)
-    # batch-1 decode with every 8B matrix in Q6_K (Q4_K_M files keep lm_head
-    # and part of attn_v / ffn_down in Q6_K)
-    per, tot_b, tot_us = [], 0, 0.0
-    for i, (name, rows, k) in enumerate(SWEEP_8B):
-        dt = pkg.Q6_K
-        copies = max(2, min(8, int(2 * 256e6 // (rows * k * bpw[dt])) + 1))
-        ws = weights_dev(dt, rows, k, SEED ^ 0x700 ^ i, 0.02, copies)
-        x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x800 ^ i, 1.0, 1, k)).cuda()
-        y = torch.empty(rows, dtype=torch.float32, device="cuda")
-        fn = lambda c: check(lib.swamp_qgemv(dt, ws[c % copies].data_ptr(), ws[0].numel(),
-                                             x.data_ptr(), y.data_ptr(), rows, k, s), "swamp_qgemv")
-        us = timed(fn)
-        b = int(rows * k * bpw[dt]) + k * 4 + rows * 4
-        per.append({"name": name, "dtype": "Q6_K", "rows": rows, "k": k, "us": round(us, 2),
-                    "GB/s": round(b / us / 1e3, 1)})
-        tot_b += b
-        tot_us += us
-        del ws, x, y
-    print(json.dumps({"sweep": "llama3-8b decode Q6_K", "n_tok": 1, "alg_bytes": tot_b,
-                      "us": round(tot_us, 1), "GB/s": round(tot_b / tot_us / 1e3, 1),
-                      "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
-                      "matrices": per}), flush=True)
+    # every 8B matrix in Q6_K (Q4_K_M files keep lm_head and part of attn_v /
+    # ffn_down in Q6_K): batch-1 decode, and small batches of 4, 16 and 32
+    # tokens (one pass each)
+    for n_tok in (1, 4, 16, 32):
+        per, tot_b, tot_us = [], 0, 0.0
+        for i, (name, rows, k) in enumerate(SWEEP_8B):
+            dt = pkg.Q6_K
+            copies = max(2, min(8, int(2 * 256e6 // (rows * k * bpw[dt])) + 1))
+            ws = weights_dev(dt, rows, k, SEED ^ 0x700 ^ i, 0.02, copies)
+            x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x800 ^ i, 1.0, n_tok, k)).cuda()
+            y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+            if n_tok == 1:
+                fn = lambda c: check(lib.swamp_qgemv(dt, ws[c % copies].data_ptr(), ws[0].numel(),
+                                                     x.data_ptr(), y.data_ptr(), rows, k, s),
+                                     "swamp_qgemv")
+            else:
+                fn = lambda c: check(lib.swamp_qgemv_batched(
+                    dt, ws[c % copies].data_ptr(), ws[0].numel(), x.data_ptr(), y.data_ptr(),
+                    n_tok, rows, k, 0, s), "swamp_qgemv_batched")
+            us = timed(fn)
+            b = int(rows * k * bpw[dt]) + n_tok * k * 4 + n_tok * rows * 4
+            per.append({"name": name, "dtype": "Q6_K", "rows": rows, "k": k, "us": round(us, 2),
+                        "GB/s": round(b / us / 1e3, 1)})
+            tot_b += b
+            tot_us += us
+            del ws, x, y
+        print(json.dumps({"sweep": "llama3-8b decode/small-batch Q6_K", "n_tok": n_tok,
+                          "alg_bytes": tot_b, "us": round(tot_us, 1),
+                          "GB/s": round(tot_b / tot_us / 1e3, 1),
+                          "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                          "matrices": per}), flush=True)
     # activation producers of the 8B prefill at 2048 tokens: RMSNorm rows and
     # SiLU(gate) * up, written as the GEMM's bf16 input
     # (input copies rotate so that more than 512 MB cycles through the cache)

@@ -179,17 +179,19 @@ SWAMP_API int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * fused_gemv_q4k_batched, fused_gemv_q4k.rs:527-554, :694).
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
- * pass of up to 64 tokens (Q4_0, Q8_0, Q4_K).  With accumulate = 0, a pass
+ * pass of up to 64 tokens (Q4_0, Q8_0, Q4_K; Q6_K 32).  With accumulate = 0, a pass
  * of one token runs the decode GEMV, and n_tok > 64 runs swamp_qgemm's
  * kernels on x rounded to bf16 (in scratch; without scratch, passes of 64
  * instead).  Passes of 2..64 tokens round x to fp16 on the matrix cores
  * (about 3e-5 of ||W_r|| ||x|| against the fp32 reference; more than 64
  * tokens, bf16: about 1e-4): entries must lie within fp16 range
- * (|x| < 65504), also for accumulate = 1 and when no scratch is available.  Q6_K:
- * forward_linear_batch sends it to fallback_gemv (linear.rs:336-364), the
- * GEMV per token written over y;
- * so here accumulate = 0 runs swamp_qgemv per token and accumulate = 1 is
- * SWAMP_EDTYPE. */
+ * (|x| < 65504), also for accumulate = 1 and when no scratch is available.  Q6_K
+ * (forward_linear_batch's fallback_gemv, linear.rs:336-364, is written over
+ * y): accumulate = 1 is SWAMP_EDTYPE; rows of a multiple of 512 weights
+ * run passes of up to 32 tokens on the matrix cores, at any n_tok, with
+ * the weights d * sc * (q - 32) rounded once to fp16 (the same precision
+ * class as the other formats' passes); other rows run swamp_qgemv per
+ * token. */
 SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
                         const float *d_x, float *d_y, int n_tok, int n_rows,
                         int n_cols, int accumulate, void *stream);

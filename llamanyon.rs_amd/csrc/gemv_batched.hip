@@ -1,5 +1,6 @@
-// gemv_batched.hip -- small-batch (2..64 tokens per pass) quantized GEMV on
-// the matrix cores, for speculative verify and continuous batching.
+// gemv_batched.hip -- small-batch (2..64 tokens per pass; Q6_K 2..32)
+// quantized GEMV on the matrix cores, for speculative verify and
+// continuous batching.  Q4_0, Q8_0, Q4_K and Q6_K weights.
 //
 // Replaces forward_linear_batch (swamp-engine/src/linear.rs:176-239) and
 // fused_gemv_q4k_batched (swamp-kernels/src/fused_gemv_q4k.rs:527-554,
@@ -65,6 +66,10 @@ __device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(
 // bytes (0, 2) or (1, 3) of one dword.
 template <int DT>
 __host__ __device__ constexpr int slot_elem(int st, int i) {
+  // Q6_K: step st takes group k = st / 2 (16 weights, one scale) and its
+  // half st % 2, 8 consecutive weights; numbered by x offset from the
+  // item's first weight (32 k + c)
+  if (DT == SWAMP_Q6_K) return 32 * (st / 2) + 8 * (st % 2) + i;
   if (DT == SWAMP_Q8_0) {
     const int p = i / 2, h = i % 2;
     // two int8 dwords per step; pair 0/1 of dword 0 -> bytes (0,2), (1,3)
@@ -81,15 +86,19 @@ __host__ __device__ constexpr int slot_elem(int st, int i) {
 }
 
 // The 8 elements of step st, as loaded by the activation staging: Q4_0 and
-// Q8_0 read elements base(st)+0..7; Q4_K reads 4st+0..3 and 32+4st+0..3.
-// slot_local gives the index (0..7) of slot i in that 8-float group.
+// Q8_0 read elements base(st)+0..7; Q4_K reads 4st+0..3 and 32+4st+0..3;
+// Q6_K reads x offsets 32(st/2) + 8(st%2) + 0..7 from the item's first
+// weight (x_item_base).  slot_local gives the index (0..7) of slot i in
+// that 8-float group.
 template <int DT>
 __host__ __device__ constexpr int stage_elem(int st, int v) {
+  if (DT == SWAMP_Q6_K) return 32 * (st / 2) + 8 * (st % 2) + v;
   if (DT == SWAMP_Q4_K) return (v < 4 ? 0 : 32) + 4 * st + (v & 3);
   return 32 * (st / 4) + 8 * (st % 4) + v;
 }
 template <int DT>
 __host__ __device__ constexpr int slot_local(int i) {
+  if (DT == SWAMP_Q6_K) return i;
   if (DT == SWAMP_Q8_0) {
     const int p = i / 2, h = i % 2;
     return 4 * (p / 2) + (p % 2) + 2 * h;
@@ -107,6 +116,18 @@ constexpr bool staging_matches_slots() {
 static_assert(staging_matches_slots<SWAMP_Q4_0>(), "Q4_0 staging order");
 static_assert(staging_matches_slots<SWAMP_Q8_0>(), "Q8_0 staging order");
 static_assert(staging_matches_slots<SWAMP_Q4_K>(), "Q4_K staging order");
+static_assert(staging_matches_slots<SWAMP_Q6_K>(), "Q6_K staging order");
+
+// Offset in x of an item's first weight: items are 64 consecutive weights,
+// except Q6_K, whose item (block b, half h, columns i) holds 4 runs of 16:
+// x[256b + 128h + 16i + 32k + c], k < 4, c < 16 (q6_k.rs:28-44).
+template <int DT>
+__device__ __forceinline__ size_t x_item_base(int item) {
+  if constexpr (DT == SWAMP_Q6_K)
+    return size_t(item >> 2) * 256 + 128 * ((item >> 1) & 1) + 16 * (item & 1);
+  else
+    return size_t(item) * 64;
+}
 
 // Q4_K per-item scales as fp16 pairs: sub-block A (item elements 0..31)
 // and B (32..63) of quarter `quarter`, W = q * s - m.
@@ -222,15 +243,81 @@ __device__ __forceinline__ half8_t weights_step(const Raw<DT> &r, int st, const 
   return v;
 }
 
+// The group scales of a Q6_K item, d * sc[8h + i + 2k] for k < 4, as fp16
+// pairs (one rounding of the exact product).  The item's windows start at
+// the block's dword-aligned address; sh (0 or 2 bytes, the block's parity)
+// realigns them.
+struct Q6kScales {
+  half2_t s[4];
+};
+__device__ __forceinline__ Q6kScales q6k_item_scales(const Raw<SWAMP_Q6_K> &r, int g,
+                                                     uint32_t sh) {
+  Q6kScales q;
+  const uint32_t ii = uint32_t(g & 1);
+  const uint32_t s01 = __builtin_amdgcn_alignbyte(r.s[1], r.s[0], sh);
+  const uint32_t s23 = __builtin_amdgcn_alignbyte(r.s[2], r.s[1], sh);
+  const float d = swamp::f16_bits_to_f32(__builtin_amdgcn_alignbyte(0u, r.d, sh) & 0xFFFFu);
+  // int8 scales: bytes i and 2 + i of each scale dword (groups 0..3)
+  const int sc[4] = {int(s01 << (24 - 8 * ii)) >> 24, int(s01 << (8 - 8 * ii)) >> 24,
+                     int(s23 << (24 - 8 * ii)) >> 24, int(s23 << (8 - 8 * ii)) >> 24};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const _Float16 v = _Float16(d * float(sc[k]));  // exact product, rounded once
+    q.s[k] = half2_t{v, v};
+  }
+  return q;
+}
+
+// 8 fp16 weights of MFMA step st of a Q6_K item, in slot_elem order: group
+// k = st / 2, columns c = 8 (st % 2) + 0..7 (dwords t0, t0 + 1 of the ql
+// and qh windows, realigned here rather than kept realigned for the whole
+// item, which would hold 12 more registers).  The 6-bit codes (low or high
+// nibble of ql, two bits of qh) become fp16 1024 + q by one byte permute
+// per pair, q - 32 exactly by the packed subtraction, then one rounding in
+// the multiply by the group scale.
+__device__ __forceinline__ half8_t weights_step_q6k(const Raw<SWAMP_Q6_K> &r, const Q6kScales &q,
+                                                    uint32_t sh, int st) {
+  const int k = st / 2, t0 = 2 * (st % 2);
+  const half2_t off = {_Float16(-1056.0f), _Float16(-1056.0f)};
+  constexpr uint32_t kSelLo = 0x04010400u, kSelHi = 0x04030402u;  // bytes (0,1) / (2,3)
+  const uint32_t mg = 0x64646464u;
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int t = t0 + j;
+    const uint32_t l = (k & 1) ? __builtin_amdgcn_alignbyte(r.b[t + 1], r.b[t], sh)
+                               : __builtin_amdgcn_alignbyte(r.a[t + 1], r.a[t], sh);
+    const uint32_t h = __builtin_amdgcn_alignbyte(r.h[t + 1], r.h[t], sh);
+    const uint32_t nib = k < 2 ? (l & 0x0F0F0F0Fu) : ((l >> 4) & 0x0F0F0F0Fu);
+    const uint32_t hb = k == 0   ? (h << 4) & 0x30303030u
+                        : k == 1 ? (h << 2) & 0x30303030u
+                        : k == 2 ? h & 0x30303030u
+                                 : (h >> 2) & 0x30303030u;
+    const uint32_t code = nib | hb;  // bytes q, 0..63
+    o[2 * j] = as_u((as_h2(__builtin_amdgcn_perm(mg, code, kSelLo)) + off) * q.s[k]);
+    o[2 * j + 1] = as_u((as_h2(__builtin_amdgcn_perm(mg, code, kSelHi)) + off) * q.s[k]);
+  }
+  half8_t v;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    half2_t h = as_h2(o[p]);
+    v[2 * p] = h[0];
+    v[2 * p + 1] = h[1];
+  }
+  return v;
+}
+
 // Bytes of 4 consecutive items (one item per lane group) and the offset of
 // a lane's item inside such a group of 4.
 template <int DT>
 __host__ __device__ constexpr uint32_t quad_bytes() {
-  return DT == SWAMP_Q4_0 ? 144u : DT == SWAMP_Q8_0 ? 272u : 144u;
+  return DT == SWAMP_Q4_0 ? 144u : DT == SWAMP_Q8_0 ? 272u : DT == SWAMP_Q6_K ? 210u : 144u;
 }
 template <int DT>
 __device__ __forceinline__ uint32_t lane_item_offset(int g) {
   if constexpr (DT == SWAMP_Q4_K) return 16u + 32u * uint32_t(g);  // quarter g after the header
+  // Q6_K: item g's ql window from the block's dword-aligned start (64 h + 16 i)
+  else if constexpr (DT == SWAMP_Q6_K) return 64u * uint32_t((g >> 1) & 1) + 16u * uint32_t(g & 1);
   else return uint32_t(g) * (quad_bytes<DT>() / 4);
 }
 
@@ -344,7 +431,7 @@ __device__ __forceinline__ void stage_x(const Args &a, half8_t *xl, int item0, i
       const int item = item0 + (r - tok * n_items);
       v0[u] = v1[u] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (e < n_ent && tok < a.n_tok && item < a.ipr) {
-        const float *xp = a.x + size_t(tok) * a.n_cols + size_t(item) * 64;
+        const float *xp = a.x + size_t(tok) * a.n_cols + x_item_base<DT>(item);
         v0[u] = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 0));
         v1[u] = *reinterpret_cast<const float4 *>(xp + stage_elem<DT>(st, 4));
       }
@@ -429,7 +516,16 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
     const int base = kitem0 + q.p * ipp + ks * a.ipw;
     const int first = base + 4 * q.c * kChunk;  // first item of the chunk
     const uint32_t soff = uint32_t(base / 4) * quad_bytes<DT>() + uint32_t(q.c) * chunk_bytes;
-    if constexpr (!kRagged) {
+    if constexpr (DT == SWAMP_Q6_K) {
+      // rows are whole 512-weight pairs of blocks (never ragged); item i of
+      // the chunk is in block soff / 210 + i, loaded from its dword-aligned
+      // start (the windows are realigned by q6k_item)
+      const int nr = first < a.ipr ? min(kRowsTile, a.n_rows - row0) : 0;
+      const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
+#pragma unroll
+      for (int i = 0; i < kChunk; i++)
+        swamp::load_raw_buf<DT>(r[i], rs, lane_off, (soff + uint32_t(i) * 210u) & ~3u, g);
+    } else if constexpr (!kRagged) {
       // ipr is a multiple of 4 * kChunk: a chunk lies wholly inside the
       // row or wholly past it (then the descriptor has no records and the
       // loads return zeros); no per-lane select before the loads
@@ -524,13 +620,21 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
     }
     const half8_t *xc = xlane + qc.c * kChunk * 32 * FR;
     Acc<NG> c = acc0;
+    // Q6_K: block of the chunk's first item (its parity gives each block's
+    // misalignment)
+    [[maybe_unused]] const int blk0 = (kitem0 + qc.p * ipp + ks * a.ipw) / 4 + qc.c * kChunk;
 #pragma unroll
     for (int i = 0; i < kChunk; i++) {
       Q4kScales kq{};
       if constexpr (DT == SWAMP_Q4_K) kq = q4k_item_scales(r[i], g);
+      Q6kScales q6{};
+      [[maybe_unused]] const uint32_t sh6 = 2u * uint32_t((blk0 + i) & 1);
+      if constexpr (DT == SWAMP_Q6_K) q6 = q6k_item_scales(r[i], g, sh6);
 #pragma unroll
       for (int st = 0; st < 8; st++) {
-        const half8_t wb = weights_step<DT>(r[i], st, kq);
+        half8_t wb;
+        if constexpr (DT == SWAMP_Q6_K) wb = weights_step_q6k(r[i], q6, sh6, st);
+        else wb = weights_step<DT>(r[i], st, kq);
         // one dequantized B fragment feeds every token group
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
@@ -634,6 +738,18 @@ int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
   return SWAMP_OK;
 }
 
+// launch_geo with the ragged form when a row's items are not a multiple of
+// the chunk granule (Q6_K rows never are: whole pairs of blocks).
+template <int DT, int TOK, int kChunk>
+int launch_geo_r(Args a, int lwk, int nkg, hipStream_t s) {
+  if constexpr (DT == SWAMP_Q6_K) {
+    return launch_geo<DT, TOK, kChunk, false>(a, lwk, nkg, s);
+  } else {
+    return a.ipr % (4 * kChunk) ? launch_geo<DT, TOK, kChunk, true>(a, lwk, nkg, s)
+                                : launch_geo<DT, TOK, kChunk, false>(a, lwk, nkg, s);
+  }
+}
+
 // K-group plan of a pass: with one wave per tile (Wk = 1) a workgroup
 // covers 16 tiles; when those tile groups fill at most half the CUs and the
 // pass's activations are not small (n_tok * K >= 16384 fp32, which the
@@ -685,13 +801,10 @@ int launch_pass_tok(Args a, hipStream_t s) {
     const KgPlan kp = kg_plan(a.n_tok, a.n_rows, a.n_cols, TOK);
     const int nkg = kp.nkg, q = kp.q;
     if (nkg > 1) {
-      if constexpr (token_groups<TOK>() == 1) {
-        if (q == 8)
-          return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, 0, nkg, s)
-                           : launch_geo<DT, TOK, 2, false>(a, 0, nkg, s);
+      if constexpr (token_groups<TOK>() == 1 && DT != SWAMP_Q6_K) {
+        if (q == 8) return launch_geo_r<DT, TOK, 2>(a, 0, nkg, s);
       }
-      return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, 0, nkg, s)
-                       : launch_geo<DT, TOK, 1, false>(a, 0, nkg, s);
+      return launch_geo_r<DT, TOK, 1>(a, 0, nkg, s);
     }
   }
   static const int forced = [] {  // tuning override: SWAMP_BATCHED_LWK (0..4)
@@ -716,14 +829,11 @@ int launch_pass_tok(Args a, hipStream_t s) {
   // else fewer slices.
   while (best > 0 && ((4 << best) > xcap || (4 << best) > a.ipr)) best--;
   // token groups keep one-item chunks: their accumulators take the registers
-  // a second item would
-  if constexpr (token_groups<TOK>() == 1) {
-    if ((8 << best) <= xcap && (8 << best) <= a.ipr)
-      return a.ipr % 8 ? launch_geo<DT, TOK, 2, true>(a, best, 1, s)
-                       : launch_geo<DT, TOK, 2, false>(a, best, 1, s);
+  // a second item would; so does Q6_K (19 registers of raw bytes per item)
+  if constexpr (token_groups<TOK>() == 1 && DT != SWAMP_Q6_K) {
+    if ((8 << best) <= xcap && (8 << best) <= a.ipr) return launch_geo_r<DT, TOK, 2>(a, best, 1, s);
   }
-  return a.ipr % 4 ? launch_geo<DT, TOK, 1, true>(a, best, 1, s)
-                   : launch_geo<DT, TOK, 1, false>(a, best, 1, s);
+  return launch_geo_r<DT, TOK, 1>(a, best, 1, s);
 }
 
 // Token count of the pass's activation layout (4, 8 or 16).
@@ -741,8 +851,9 @@ int launch_pass(Args a, hipStream_t s) {
   if (a.n_tok <= 4) return launch_pass_tok<DT, 4>(a, s);
   if (a.n_tok <= 8) return launch_pass_tok<DT, 8>(a, s);
   if (a.n_tok <= 16) return launch_pass_tok<DT, 16>(a, s);
-  if (a.n_tok <= 32) return launch_pass_tok<DT, 32>(a, s);
-  return launch_pass_tok<DT, 64>(a, s);
+  if (a.n_tok <= 32 || DT == SWAMP_Q6_K) return launch_pass_tok<DT, 32>(a, s);
+  if constexpr (DT != SWAMP_Q6_K) return launch_pass_tok<DT, 64>(a, s);
+  return SWAMP_ESHAPE;
 }
 
 }  // namespace
@@ -750,15 +861,21 @@ int launch_pass(Args a, hipStream_t s) {
 namespace {
 
 // Tokens per pass of the small-batch kernel: up to 64 (four token groups
-// per weight fragment).
-int pass_len(uint32_t) { return kTok; }
+// per weight fragment); Q6_K up to 32 (four groups of Q6_K items do not fit
+// the 128 registers a lane has at 16 waves per CU).
+int pass_len(uint32_t dtype) { return dtype == SWAMP_Q6_K ? 32 : kTok; }
 
 // The GEMM route of a call: more than 64 tokens written over y, on x rounded
-// to bf16 (in scratch).
-bool gemm_route(int n_tok, int n_cols, int accumulate) {
-  return n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
+// to bf16 (in scratch).  Q6_K stays on the passes at any count: its GEMM
+// needs a bf16 copy of the weights in scratch, which the passes do not.
+bool gemm_route(uint32_t dtype, int n_tok, int n_cols, int accumulate) {
+  return dtype != SWAMP_Q6_K && n_tok > kTok && !accumulate && n_cols % 64 == 0 &&
          size_t(n_tok) * size_t(n_cols) * 2 <= size_t(UINT32_MAX);
 }
+
+// Q6_K rows the passes take: whole pairs of blocks (4-byte aligned rows);
+// other rows run the decode GEMV per token.
+bool q6k_passes(int n_cols) { return n_cols % 512 == 0; }
 
 // Scratch of the small-batch passes: the largest K-group partial block.
 size_t kgroup_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols, int accumulate) {
@@ -778,8 +895,10 @@ size_t kgroup_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols, int accum
 size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols,
                                    int accumulate, size_t limit) {
   if (n_tok <= 0 || n_rows <= 0 || n_cols <= 0) return 0;
-  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return 0;
-  if (gemm_route(n_tok, n_cols, accumulate)) {
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K && dtype != SWAMP_Q6_K)
+    return 0;
+  if (dtype == SWAMP_Q6_K && (accumulate || !q6k_passes(n_cols))) return 0;
+  if (gemm_route(dtype, n_tok, n_cols, accumulate)) {
     const size_t xb = (size_t(n_tok) * size_t(n_cols) * 2 + 255) & ~size_t(255);
     return xb + swamp_gemm_scratch_bytes(dtype, SWAMP_BF16, n_tok, n_rows, n_cols,
                                          limit > xb ? limit - xb : 0);
@@ -791,10 +910,11 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
                               int n_tok, int n_rows, int n_cols, int accumulate,
                               swamp::Scratch &sc, hipStream_t s) {
   if (n_rows == 0 || n_tok == 0) return SWAMP_OK;
-  if (dtype == SWAMP_Q6_K) {
-    // forward_linear_batch sends Q6_K to fallback_gemv (linear.rs:336-364):
-    // fused_gemv_q6k per token, written over the output (:357, :361)
-    if (accumulate) return SWAMP_EDTYPE;
+  if (dtype == SWAMP_Q6_K && accumulate) return SWAMP_EDTYPE;
+  if (dtype == SWAMP_Q6_K && !q6k_passes(n_cols)) {
+    // rows of an odd number of blocks: the decode GEMV per token, written
+    // over y, as forward_linear_batch's fallback_gemv does for every Q6_K
+    // row (linear.rs:336-364)
     for (int t = 0; t < n_tok; t++) {
       const int rc = swamp_launch_gemv(dtype, d_w, d_x + size_t(t) * n_cols,
                                        d_y + size_t(t) * n_rows, n_rows, n_cols, s);
@@ -805,7 +925,7 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   // Batches of more than 64 tokens written over y run as the prefill GEMM
   // on x rounded to bf16 (in scratch).  Without scratch the passes below
   // run instead.
-  if (gemm_route(n_tok, n_cols, accumulate)) {
+  if (gemm_route(dtype, n_tok, n_cols, accumulate)) {
     const size_t n = size_t(n_tok) * size_t(n_cols);
     if (void *xb = sc.get(n * 2)) {
       int rc = swamp_launch_f32_to_bf16(d_x, xb, n, s);
@@ -823,7 +943,8 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
   a.accumulate = accumulate;
   // 16 rows of a tile are addressed by one buffer descriptor (32-bit range)
   if (size_t(a.row_bytes) * kRowsTile >= (size_t(1) << 30)) return SWAMP_ESHAPE;
-  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K) return SWAMP_EDTYPE;
+  if (dtype != SWAMP_Q4_0 && dtype != SWAMP_Q8_0 && dtype != SWAMP_Q4_K && dtype != SWAMP_Q6_K)
+    return SWAMP_EDTYPE;
   // scratch for the passes that split K over workgroups; without it the
   // passes run as K phases
   const size_t ws_bytes = kgroup_bytes(dtype, n_tok, n_rows, n_cols, accumulate);
@@ -843,6 +964,7 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     switch (dtype) {
     case SWAMP_Q4_0: rc = launch_pass<SWAMP_Q4_0>(a, s); break;
     case SWAMP_Q8_0: rc = launch_pass<SWAMP_Q8_0>(a, s); break;
+    case SWAMP_Q6_K: rc = launch_pass<SWAMP_Q6_K>(a, s); break;
     default: rc = launch_pass<SWAMP_Q4_K>(a, s); break;
     }
   }

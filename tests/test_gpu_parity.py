@@ -13,7 +13,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K, F32, F16, BF16 = 2, 8, 12, 0, 1, 30
+Q4_0, Q8_0, Q4_K, Q6_K, F32, F16, BF16 = 2, 8, 12, 14, 0, 1, 30
 TOL = 1e-3
 SEED = 0x5EED
 
@@ -293,7 +293,8 @@ def test_batched_repeat_bitwise(pkg, torch_dev):
     each launch leaves at zero: repeated calls, with other shapes (and a
     larger workspace) in between, give bit-identical results."""
     torch = torch_dev
-    shapes = [(Q4_K, 16, 4096, 14336), (Q8_0, 7, 6144, 4096), (Q4_0, 16, 300, 4096)]
+    shapes = [(Q4_K, 16, 4096, 14336), (Q8_0, 7, 6144, 4096), (Q4_0, 16, 300, 4096),
+              (Q6_K, 12, 4096, 14336)]
     first = []
     bufs = []
     for i, (dt, n_tok, rows, cols) in enumerate(shapes):
@@ -324,7 +325,7 @@ def test_batched_two_streams(pkg, torch_dev):
     # GEMM route: bf16 x in one per-stream buffer, K pieces in the other
     cases = [(Q4_K, 16, 4096, 14336), (Q4_0, 8, 6144, 4096), (Q8_0, 12, 4096, 4096),
              (Q4_0, 40, 4096, 4096), (Q4_K, 64, 6144, 4096), (Q4_0, 80, 4096, 4096),
-             (Q4_K, 96, 6144, 4096)]
+             (Q4_K, 96, 6144, 4096), (Q6_K, 32, 4096, 14336)]
     bufs = []
     for i, (dt, n_tok, rows, cols) in enumerate(cases):
         raw = weights(pkg, dt, rows, cols, mid=120 + i)
@@ -511,10 +512,10 @@ def test_gemm_int8_argument_errors(pkg, torch_dev):
         pkg.qgemm(Q4_0, d_w.data_ptr(), raw.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m, rows,
                   cols, stream(torch))
     assert e.value.code == pkg.ESHAPE
-    rawk = weights(pkg, pkg.Q6_K, rows, 512)
+    rawk = weights(pkg, Q6_K, rows, 512)
     d_wk = up(torch, rawk)
     with pytest.raises(pkg.GpuError) as e:
-        pkg.qgemm(pkg.Q6_K, d_wk.data_ptr(), rawk.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m,
+        pkg.qgemm(Q6_K, d_wk.data_ptr(), rawk.size, d_q.data_ptr(), Q8_0, d_y.data_ptr(), m,
                   rows, 512, stream(torch))
     assert e.value.code == pkg.EDTYPE
     torch.cuda.synchronize()

@@ -178,30 +178,84 @@ def test_q6k_multi_mixed_with_q4k(pkg, orc, torch_dev):
             assert orc.normalized_error(down(d_y), ref, deq, x) <= TOL, (dt, r, cols)
 
 
-@pytest.mark.parametrize("n_tok,rows,cols", [(1, 300, 4096), (5, 1000, 4096), (17, 64, 14336),
-                                             (3, 40, 768)])
-def test_q6k_batched_is_per_token(pkg, orc, torch_dev, n_tok, rows, cols):
-    """forward_linear_batch on Q6_K = fallback_gemv: the GEMV per token,
-    written over y (linear.rs:336-364); the accumulating form is refused."""
+def _batched(pkg, torch, raw, xs, rows, cols, accumulate=False, base=None):
+    n_tok = xs.shape[0]
+    d_w, d_x = up(torch, raw), up(torch, xs)
+    if base is None:
+        d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    else:
+        d_y = up(torch, base)
+    pkg.qgemv_batched(Q6_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                      rows, cols, accumulate, stream(torch))
+    torch.cuda.synchronize()
+    return down(d_y)
+
+
+def _batched_err(pkg, orc, raw, xs, y, rows, cols, sel=None):
+    rb = pkg.row_bytes(Q6_K, cols)
+    worst = 0.0
+    for r0, r1 in sel or [(0, rows)]:
+        sub = raw[r0 * rb:r1 * rb]
+        ref = orc.forward_linear_batch(Q6_K, sub, xs, r1 - r0, cols, 8)
+        deq = orc.dequantize(Q6_K, sub, (r1 - r0) * cols).reshape(r1 - r0, cols)
+        worst = max(worst, orc.normalized_error(y[:, r0:r1], ref, deq, xs))
+    return worst
+
+
+# passes on the matrix cores for rows of a multiple of 512 weights: up to 32
+# tokens each (2..4 tokens, 5..8, 9..16, 17..32 in two token groups), K
+# groups (1024 x 14336), K phases (32 tokens x 14336), a 70-token call in
+# three passes (32 + 32 + 6); one token and rows of an odd number of blocks
+# (768) run the decode GEMV per token
+@pytest.mark.parametrize("n_tok,rows,cols", [(1, 300, 4096), (2, 77, 512), (5, 1000, 4096),
+                                             (16, 1024, 14336), (17, 64, 14336),
+                                             (32, 2000, 4096), (32, 100, 14336),
+                                             (70, 256, 2048), (3, 40, 768)])
+def test_q6k_batched(pkg, orc, torch_dev, errlog, n_tok, rows, cols):
+    """forward_linear_batch on Q6_K, written over y (linear.rs:336-364):
+    within the batched fp16 bound (1e-4; x and the weights rounded to fp16
+    once) against the oracle's per-token GEMV; the one-token pass and the
+    odd-block rows are swamp_qgemv bit for bit; accumulate is refused."""
     torch = torch_dev
-    raw = weights(pkg, Q6_K, rows, cols, mid=n_tok)
+    raw = weights(pkg, Q6_K, rows, cols, mid=n_tok ^ rows)
     xs = acts(pkg, n_tok, cols, mid=n_tok)
     say("q6k batched", n_tok, rows, cols)
+    y = _batched(pkg, torch, raw, xs, rows, cols)
+    assert np.all(np.isfinite(y))
+    err = errlog(f"q6k batched n_tok={n_tok} {rows}x{cols}",
+                 _batched_err(pkg, orc, raw, xs, y, rows, cols), path="batched_f16")
+    per_token = n_tok == 1 or cols % 512 != 0
+    assert err <= (1e-5 if per_token else 1e-4)
+    if per_token:
+        for t in range(n_tok):
+            assert np.array_equal(_gemv(pkg, torch, raw, xs[t], rows, cols), y[t])
     d_w, d_x = up(torch, raw), up(torch, xs)
-    d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
-    pkg.qgemv_batched(Q6_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
-                      rows, cols, False, stream(torch))
-    torch.cuda.synchronize()
-    y = down(d_y)
-    ref = orc.forward_linear_batch(Q6_K, raw, xs, rows, cols, 8)
-    deq = orc.dequantize(Q6_K, raw, rows * cols).reshape(rows, cols)
-    assert orc.normalized_error(y, ref, deq, xs) <= TOL
-    single = _gemv(pkg, torch, raw, xs[-1], rows, cols)
-    assert np.array_equal(single, y[-1])
+    d_y = torch.zeros((n_tok, rows), dtype=torch.float32, device="cuda")
     with pytest.raises(pkg.GpuError) as e:
         pkg.qgemv_batched(Q6_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
                           rows, cols, True, stream(torch))
     assert e.value.code == pkg.EDTYPE
+
+
+@pytest.mark.parametrize("n_tok", [4, 16, 32])
+def test_q6k_batched_lm_head_subsets(pkg, orc, torch_dev, errlog, n_tok):
+    """Llama-3 8B lm_head, 128256 x 4096 Q6_K (as Q4_K_M files keep it), in
+    one pass: the oracle on three row ranges; every token's rows equal the
+    same call's rows with the tokens reversed (the pass is per-token exact
+    in its order of sums, whatever the token's slot)."""
+    torch = torch_dev
+    rows, cols = 128256, 4096
+    raw = weights(pkg, Q6_K, rows, cols, mid=3)
+    xs = acts(pkg, n_tok, cols, mid=n_tok + 100)
+    say("q6k batched lm_head", n_tok)
+    y = _batched(pkg, torch, raw, xs, rows, cols)
+    assert np.all(np.isfinite(y))
+    sel = [(0, 512), (rows // 2, rows // 2 + 256), (rows - 512, rows)]
+    err = errlog(f"q6k batched lm_head n_tok={n_tok}",
+                 _batched_err(pkg, orc, raw, xs, y, rows, cols, sel=sel), path="batched_f16")
+    assert err <= 1e-4
+    y_rev = _batched(pkg, torch, raw, np.ascontiguousarray(xs[::-1]), rows, cols)
+    assert np.array_equal(y_rev[::-1], y)
 
 
 def test_q6k_gguf_upload_then_gemv(pkg, orc, torch_dev, tmp_path):

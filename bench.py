@@ -37,7 +37,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--cpu-threads 6,max] [--sweep] [--pmc-probe] [--pmc-gemm]
                        [--pmc-batched N]
 --sweep adds one JSON line per extra workload after the main line: the
-Q4_K small-batch sweep (1/4/8/16/17/24/32/64 tokens; 17-64 in token groups
+Q4_K small-batch sweep (1/2/4/8/16/17/24/32/64 tokens; 2 as one GEMV, 17-64 in token groups
 of 16) at 8B shapes and the 70B layer
 (decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
@@ -278,9 +278,9 @@ SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 81
 
 def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
-    (lm_head Q8_0) for 1, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
+    (lm_head Q8_0) for 1, 2, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
     groups of 16), the 70B Q4_K layer as
-    batch-1 decode, the 8B shapes in Q6_K at 1, 4, 16 and 32 tokens, the 70B
+    batch-1 decode, the 8B shapes in Q6_K at 1, 2, 4, 16 and 32 tokens, the 70B
     layer as a 4096-token bf16 prefill GEMM, and the 8B layer (without
     lm_head) as a 2048-token int8 GEMM with Q4_K and Q4_0 weights.  Each matrix is
     timed alone: 20 launches over 3 rotated weight copies behind a GPU
@@ -311,7 +311,7 @@ def run_sweep(pkg, torch, np, stream, lib):
             raise pkg.GpuError(rc, what)
 
     for label, shapes, sigma in (("llama3-8b", SWEEP_8B, 0.02), ("llama3-70b", SWEEP_70B, 0.015)):
-        for n_tok in ((1, 4, 8, 16, 17, 24, 32, 64) if label == "llama3-8b" else (1,)):
+        for n_tok in ((1, 2, 4, 8, 16, 17, 24, 32, 64) if label == "llama3-8b" else (1,)):
             per, tot_b, tot_us = [], 0, 0.0
             for i, (name, rows, k) in enumerate(shapes):
                 dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
@@ -342,9 +342,9 @@ def run_sweep(pkg, torch, np, stream, lib):
                               "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
                               "matrices": per}), flush=True)
     # every 8B matrix in Q6_K (Q4_K_M files keep lm_head and part of attn_v /
-    # ffn_down in Q6_K): batch-1 decode, and small batches of 4, 16 and 32
+    # ffn_down in Q6_K): batch-1 decode, and small batches of 2, 4, 16 and 32
     # tokens (one pass each)
-    for n_tok in (1, 4, 16, 32):
+    for n_tok in (1, 2, 4, 16, 32):
         per, tot_b, tot_us = [], 0, 0.0
         for i, (name, rows, k) in enumerate(SWEEP_8B):
             dt = pkg.Q6_K

@@ -180,7 +180,9 @@ SWAMP_API int swamp_qgemv_swiglu(uint32_t dtype, const void *d_w, size_t w_len,
  * Replaces forward_linear_batch (linear.rs:176-239) and
  * fused_gemv_q4k_batched.  Any n_tok >= 1; weights are read once per
  * pass of up to 64 tokens (Q4_0, Q8_0, Q4_K; Q6_K 32).  With accumulate = 0, a pass
- * of one token runs the decode GEMV, and n_tok > 64 runs swamp_qgemm's
+ * of one token runs the decode GEMV, a pass of two the GEMV over both
+ * tokens (x rounded to fp16 like the passes of 3..64, rows of up to 32768
+ * weights), and n_tok > 64 runs swamp_qgemm's
  * kernels on x rounded to bf16 (in scratch; without scratch, passes of 64
  * instead).  Passes of 2..64 tokens round x to fp16 on the matrix cores
  * (about 3e-5 of ||W_r|| ||x|| against the fp32 reference; more than 64

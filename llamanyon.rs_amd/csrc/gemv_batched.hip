@@ -884,6 +884,7 @@ size_t kgroup_bytes(uint32_t dtype, int n_tok, int n_rows, int n_cols, int accum
   for (int t0 = 0; t0 < n_tok; t0 += pl) {
     const int nt = std::min(pl, n_tok - t0);
     if (nt == 1 && !accumulate) continue;  // the decode GEMV
+    if (!accumulate && swamp_gemv_tokens_ok(dtype, nt, n_cols)) continue;  // 2 tokens
     const int nkg = pass_kgroups(nt, n_rows, n_cols);
     if (nkg > 1) ws = std::max(ws, size_t(nkg) * nt * n_rows * sizeof(float));
   }
@@ -959,6 +960,12 @@ int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w, const float *d_x,
     // streams the weights faster (8B Q4_K gate+up 15 us against 21 us here)
     if (a.n_tok == 1 && !accumulate) {
       rc = swamp_launch_gemv(dtype, d_w, a.x, a.y, n_rows, n_cols, s);
+      continue;
+    }
+    // 2 tokens written over y: the GEMV over both at once, each weight
+    // item dequantized once (fp16 x, as the passes below)
+    if (!accumulate && swamp_gemv_tokens_ok(dtype, a.n_tok, n_cols)) {
+      rc = swamp_launch_gemv_tokens(dtype, d_w, a.x, a.y, a.n_tok, n_rows, n_cols, s);
       continue;
     }
     switch (dtype) {

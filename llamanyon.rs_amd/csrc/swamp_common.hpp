@@ -140,7 +140,7 @@ inline Scratch stream_scratch(hipStream_t s, size_t bytes) {
 }  // namespace swamp
 
 // Internal launchers (defined in dequant.hip, gemv.hip, gemv_fused.hip,
-// gemv_batched.hip, gemm.hip, gemm_i8.hip, producers.hip).  They
+// gemv_tokens.hip, gemv_batched.hip, gemm.hip, gemm_i8.hip, producers.hip).  They
 // assume the arguments have been validated by api.cpp.
 int swamp_launch_dequant(uint32_t dtype, const void *d_raw, float *d_dst,
                          size_t n, hipStream_t s);
@@ -150,6 +150,12 @@ int swamp_launch_gemv(uint32_t dtype, const void *d_w, const float *d_x,
                       float *d_y, int n_rows, int n_cols, hipStream_t s);
 int swamp_launch_gemv_f16x(uint32_t dtype, const void *d_w, const float *d_x,
                            float *d_y, int n_rows, int n_cols, hipStream_t s);
+// 2 tokens at once through the fp16-x GEMV (gemv_tokens.hip), y written
+// [n_tok][n_rows]; SWAMP_ESHAPE (nothing launched) outside the shapes
+// swamp_gemv_tokens_ok accepts.
+bool swamp_gemv_tokens_ok(uint32_t dtype, int n_tok, int n_cols);
+int swamp_launch_gemv_tokens(uint32_t dtype, const void *d_w, const float *d_x, float *d_y,
+                             int n_tok, int n_rows, int n_cols, hipStream_t s);
 int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes,
                             const void *const *d_ws, const int *row_counts,
                             const float *d_x, float *const *d_ys, int n_cols,

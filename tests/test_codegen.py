@@ -134,7 +134,8 @@ def _gemm_wait_problems(body):
     return probs
 
 
-_TUS = ["api.hip", "device.hip", "dequant.hip", "gemv.hip", "gemv_fused.hip", "gemv_batched.hip",
+_TUS = ["api.hip", "device.hip", "dequant.hip", "gemv.hip", "gemv_fused.hip", "gemv_tokens.hip",
+        "gemv_batched.hip",
         "gemm.hip", "gemm_dq.hip",
         "gemm_i8.hip", "gguf.hip", "producers.hip"]
 

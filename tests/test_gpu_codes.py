@@ -12,7 +12,11 @@ back one column at a time, so each output is a single decoded weight:
     call): y[t, r] = W16[r, j0 + t], the weight rounded once to fp16,
     exactly; W16 is built here from the block fields: fp16(d (q - 8)) for Q4_0,
     fp16(d q) for Q8_0, and for Q4_K fp16(q s - m) with s = fp16(d sc), m =
-    fp16(dmin m), the scale pair rounded to fp16 as the kernel forms it.
+    fp16(dmin m), the scale pair rounded to fp16 as the kernel forms it;
+  * small batch of 2 tokens (the GEMV over both tokens: exact fp16 weight
+    pairs 1024 + q times fp16 x scaled by a power of two, the offset taken
+    off with the same x): y[t, r] = W[r, j0 + t] as for the decode GEMV,
+    Q6_K included (d sc (q - 32) has at most 24 significant bits).
 
 The quantized bytes are random (every code at every byte position), block
 scales come from the host quantizer."""
@@ -21,7 +25,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K = 2, 8, 12
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
 SEED = 0xC0DE
 
 
@@ -39,10 +43,11 @@ def random_codes(pkg, dtype, rows, cols, seed):
     """Quantizer scales, random code bytes (Q4_K: random 6-bit scale bytes too)."""
     raw = pkg.synth_quantized(dtype, seed, 0.02, rows, cols).copy()
     rng = np.random.default_rng(seed)
-    blk = {Q4_0: 18, Q8_0: 34, Q4_K: 144}[dtype]
-    first = {Q4_0: 2, Q8_0: 2, Q4_K: 4}[dtype]
+    blk = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}[dtype]
+    first = {Q4_0: 2, Q8_0: 2, Q4_K: 4, Q6_K: 0}[dtype]
+    last = blk - 2 if dtype == Q6_K else blk  # Q6_K keeps its d (the last 2 bytes)
     b = raw.reshape(-1, blk)
-    b[:, first:] = rng.integers(0, 256, size=(b.shape[0], blk - first), dtype=np.uint8)
+    b[:, first:last] = rng.integers(0, 256, size=(b.shape[0], last - first), dtype=np.uint8)
     return raw
 
 
@@ -134,3 +139,31 @@ def test_batched_one_hot_columns(pkg, orc, torch_dev, dtype):
                           rows, cols, 0, s)
         got[:, j0:j0 + n_tok] = d_y.cpu().numpy().T
     assert np.array_equal(got, w16), float(np.max(np.abs(got - w16)))
+
+
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K, Q6_K])
+def test_token_gemv_one_hot_columns(pkg, orc, torch_dev, dtype):
+    torch = torch_dev
+    n_tok = 2
+    rows, cols = 300, 512
+    raw = random_codes(pkg, dtype, rows, cols, SEED ^ 0x200 ^ dtype)
+    deq = orc.dequantize(dtype, raw, rows * cols).reshape(rows, cols)
+    print(f"[gpu case] token gemv one-hot columns dtype {dtype} n_tok {n_tok}", flush=True)
+    s = torch.cuda.current_stream().cuda_stream
+    d_w = torch.from_numpy(raw).cuda()
+    d_x = torch.zeros((n_tok, cols), dtype=torch.float32, device="cuda")
+    d_y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+    got = np.empty((rows, cols), dtype=np.float32)
+    for j0 in range(0, cols, n_tok):
+        d_x.zero_()
+        nt = min(n_tok, cols - j0)
+        for t in range(nt):
+            d_x[t, j0 + t] = 1.0
+        pkg.qgemv_batched(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                          rows, cols, 0, s)
+        got[:, j0:j0 + nt] = d_y.cpu().numpy().T[:, :nt]
+    if dtype == Q4_K:
+        tol = 4 * np.spacing(np.maximum(np.abs(deq), np.float32(1e-30)))
+        assert np.all(np.abs(got - deq) <= tol), float(np.max(np.abs(got - deq) / tol))
+    else:
+        assert np.array_equal(got, deq), float(np.max(np.abs(got - deq)))

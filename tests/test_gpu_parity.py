@@ -242,12 +242,13 @@ def test_gemv_multi(pkg, orc, torch_dev):
 # ------------------------------------------------------------ small batch
 
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
-@pytest.mark.parametrize("n_tok", [1, 4, 8, 16, 19, 33, 64, 70])
+@pytest.mark.parametrize("n_tok", [1, 2, 4, 8, 16, 19, 33, 64, 70])
 @pytest.mark.parametrize("rows,cols", [(1000, 4096), (256, 14336)])
 def test_batched_parity(pkg, orc, torch_dev, errlog, dtype, n_tok, rows, cols):
-    # 1 token: the decode GEMV; 2..64: the small-batch kernel (19 in two
-    # token groups of 16, 33 and 64 in four), x rounded to fp16; 70: the
-    # prefill GEMM on bf16-rounded x
+    # 1 token: the decode GEMV; 2: the GEMV over both tokens, x rounded to
+    # fp16; 4..64: the small-batch kernel (19 in two token groups of 16, 33
+    # and 64 in four), x rounded to fp16; 70: the prefill GEMM on
+    # bf16-rounded x
     torch = torch_dev
     raw = weights(pkg, dtype, rows, cols, mid=n_tok)
     xs = acts(pkg, n_tok, cols, mid=n_tok)

@@ -348,6 +348,7 @@ struct Args {
   int ipr;         // items (64 weights) per row
   int ipw;         // items per wave and phase (multiple of 4 * kChunk)
   int lwk;         // log2 of Wk, the waves that share one tile (K slices)
+  int wtu;         // tile lanes in use (<= 16 / Wk): a tile group's tiles
   int phases;      // K phases; phase p covers items [p*ipp, p*ipp + ipp), ipp = ipw * Wk
   int accumulate;  // y += W x instead of y = W x
   int nkg;         // K groups: workgroups split the row's items into nkg ranges
@@ -470,8 +471,12 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const int wk = 1 << a.lwk, wt = kWaves >> a.lwk;
+  // tile lanes in use: wt = 16 / Wk, or fewer so that the tile groups of
+  // one round cover every CU; the waves of a lane past wt load nothing and
+  // store nothing (they keep pace with the barriers)
+  const int wk = 1 << a.lwk, wt = a.wtu;
   const int tl = wave >> a.lwk, ks = wave & (wk - 1);
+  const bool lane_used = tl < wt;
   const int ipp = a.ipw << a.lwk;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
   const int n_tg = (n_tiles + wt - 1) / wt;
@@ -520,7 +525,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       // rows are whole 512-weight pairs of blocks (never ragged); item i of
       // the chunk is in block soff / 210 + i, loaded from its dword-aligned
       // start (the windows are realigned by q6k_item)
-      const int nr = first < a.ipr ? min(kRowsTile, a.n_rows - row0) : 0;
+      const int nr = first < a.ipr && lane_used ? min(kRowsTile, a.n_rows - row0) : 0;
       const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
 #pragma unroll
       for (int i = 0; i < kChunk; i++)
@@ -529,13 +534,13 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
       // ipr is a multiple of 4 * kChunk: a chunk lies wholly inside the
       // row or wholly past it (then the descriptor has no records and the
       // loads return zeros); no per-lane select before the loads
-      const int nr = first < a.ipr ? min(kRowsTile, a.n_rows - row0) : 0;
+      const int nr = first < a.ipr && lane_used ? min(kRowsTile, a.n_rows - row0) : 0;
       const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
 #pragma unroll
       for (int i = 0; i < kChunk; i++)
         load_item<DT>(r[i], rs, lane_off + uint32_t(i) * quad_bytes<DT>(), soff, g);
     } else {
-      const int nr = min(kRowsTile, a.n_rows - row0);
+      const int nr = lane_used ? min(kRowsTile, a.n_rows - row0) : 0;
       const __amdgpu_buffer_rsrc_t rs = swamp::make_rsrc(a.w + size_t(row0) * rb, uint32_t(nr) * rb);
 #pragma unroll
       for (int i = 0; i < kChunk; i++) {
@@ -571,7 +576,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemv_batched_kernel(Args a) {
   auto emit_tile = [&](int batch, int k, const Acc<NG> &v) {
     const int tile = tile_of(batch, k);
     if (wk == 1) {
-      if (tile < n_tiles) {
+      if (tile < n_tiles && lane_used) {
 #pragma unroll
         for (int gi = 0; gi < NG; gi++)
 #pragma unroll
@@ -724,8 +729,14 @@ int launch_geo(Args a, int lwk, int nkg, hipStream_t s) {
   a.ipw = ipp / wk;
   a.lwk = lwk;
   const int n_tiles = (a.n_rows + kRowsTile - 1) / kRowsTile;
-  const int n_tg = (n_tiles + (kWaves >> lwk) - 1) / (kWaves >> lwk);
-  const int grid = (a.nkg > 1 ? n_tg : std::min(n_tg, swamp::device_info().num_cus)) * a.nkg;
+  const int cus = swamp::device_info().num_cus;
+  // Tile groups of 16 / Wk tiles; when one round of them leaves CUs idle
+  // (8B gate+up: 224 groups of 8), groups of fewer tiles spread the round
+  // over every CU (256 of 7).  K-group plans keep their 16-tile groups.
+  a.wtu = kWaves >> lwk;
+  if (a.nkg == 1 && (n_tiles + a.wtu - 1) / a.wtu < cus) a.wtu = (n_tiles + cus - 1) / cus;
+  const int n_tg = (n_tiles + a.wtu - 1) / a.wtu;
+  const int grid = (a.nkg > 1 ? n_tg : std::min(n_tg, cus)) * a.nkg;
   const size_t lds = size_t(ipp) * 8 * frag_row<TOK>() * 16 + (wk > 1 ? kSlotBytes : 0);
   kern<<<unsigned(grid), kThreads, lds, s>>>(a);
   if (hipGetLastError() != hipSuccess) return SWAMP_ELAUNCH;

@@ -203,14 +203,16 @@ def _batched_err(pkg, orc, raw, xs, y, rows, cols, sel=None):
 
 
 # passes on the matrix cores for rows of a multiple of 512 weights: up to 32
-# tokens each (2..4 tokens, 5..8, 9..16, 17..32 in two token groups), K
+# tokens each (3..4 tokens, 5..8, 9..16, 17..32 in two token groups), K
 # groups (1024 x 14336), K phases (32 tokens x 14336), a 70-token call in
-# three passes (32 + 32 + 6); one token and rows of an odd number of blocks
-# (768) run the decode GEMV per token
+# three passes (32 + 32 + 6), one block pair per row (512); two tokens run
+# the GEMV over both; one token and rows of an odd number of blocks (768)
+# run the decode GEMV per token
 @pytest.mark.parametrize("n_tok,rows,cols", [(1, 300, 4096), (2, 77, 512), (5, 1000, 4096),
                                              (16, 1024, 14336), (17, 64, 14336),
                                              (32, 2000, 4096), (32, 100, 14336),
-                                             (70, 256, 2048), (3, 40, 768)])
+                                             (70, 256, 2048), (3, 40, 768), (5, 33, 512),
+                                             (9, 200, 1024), (2, 40, 768)])
 def test_q6k_batched(pkg, orc, torch_dev, errlog, n_tok, rows, cols):
     """forward_linear_batch on Q6_K, written over y (linear.rs:336-364):
     within the batched fp16 bound (1e-4; x and the weights rounded to fp16

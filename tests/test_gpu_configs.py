@@ -175,6 +175,31 @@ def test_config3_small_batch(pkg, orc, torch_dev, W, errlog, name, dtype, rows, 
     assert err <= min(TOL, BOUND[path])
 
 
+BATCH70_CASES = [(n, Q4_K) + LLAMA70B[n] for n in ("qkv", "gate_up", "down")]
+
+
+@pytest.mark.parametrize("n_tok", [2, 4, 16])
+@pytest.mark.parametrize("name,dtype,rows,cols", BATCH70_CASES, ids=[c[0] for c in BATCH70_CASES])
+def test_small_batch_70b_shapes(pkg, orc, torch_dev, W, errlog, name, dtype, rows, cols, n_tok):
+    """The small batch at the 70B layer's Q4_K shapes (K = 8192 and 28672):
+    the two-token GEMV with two-wave rows, and the matrix-core passes with
+    tile groups narrowed to cover every CU (gate+up: 3584 tiles)."""
+    torch = torch_dev
+    raw, d_w = W.get(dtype, rows, cols, 0.015)
+    xs = pkg.fill_normal(0xA11CE ^ (n_tok << 12) ^ rows, 1.0, n_tok, cols)
+    print(f"[gpu case] small batch 70b {name} {rows}x{cols} n_tok {n_tok}", flush=True)
+    d_x = torch.from_numpy(xs).cuda()
+    d_y = torch.full((n_tok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    pkg.qgemv_batched(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok,
+                      rows, cols, False, stream(torch))
+    torch.cuda.synchronize()
+    y = d_y.cpu().numpy()
+    assert np.isfinite(y).all()
+    err = errlog(f"small batch 70b {name} n_tok={n_tok}",
+                 check_rows(pkg, orc, dtype, raw, cols, y, xs, rows), path="batched_f16")
+    assert err <= min(TOL, BOUND["batched_f16"])
+
+
 # ------------------------------------------------------------ prefill GEMM
 
 def _gemm(pkg, orc, torch, W, dtype, sigma, rows, cols, m, x_type, mid):

@@ -456,6 +456,37 @@ ROUTE_SHAPES = [("gate_up", 28672, 4096), ("down", 4096, 14336), ("qkv", 6144, 4
 ROUTE_MS = (256, 512, 1024, 2048)
 
 
+def stream_reference(torch):
+    """torch's own streaming kernels over 1 GiB of fp32 on this device, as a
+    reference for what a plain kernel streams from HBM: sum and amax read
+    the buffer once, copy reads it and writes another.  Two buffers
+    alternate, 3 untimed calls, then the mean of 20 timed with events."""
+    n = 1 << 28
+    xs = [torch.randn(n, device="cuda") for _ in range(2)]
+    dst = torch.empty_like(xs[0])
+
+    def timed(fn, reps=20):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    out = {"stream_ref": "torch kernels over 1 GiB fp32", "bytes_read": 4 * n}
+    for name, fn, moved in (("sum", lambda i: xs[i % 2].sum(), 4 * n),
+                            ("amax", lambda i: xs[i % 2].amax(), 4 * n),
+                            ("copy", lambda i: dst.copy_(xs[i % 2]), 8 * n)):
+        t = timed(fn)
+        out[name] = {"us": round(t * 1e6, 1), "GB/s": round(moved / t / 1e9, 1),
+                     "frac_hbm_peak": round(moved / t / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def route_times(pkg, torch, s):
     """us per swamp_qgemm call (Q4_0 weights, bf16 x; mean of 20 after 10
     warm-up calls) for each 8B shape and prompt length, through whichever
@@ -547,6 +578,10 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
+    ap.add_argument("--stream-ref", action="store_true",
+                    help="only time torch's own streaming kernels over 1 GiB of fp32 (sum and "
+                         "amax: one read; copy: one read and one write) as a reference for the "
+                         "decode GEMV's weight stream; one JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -572,6 +607,9 @@ def main():
 
     if args.route_times:
         print(json.dumps(route_times(pkg, torch, s)), flush=True)
+        return
+    if args.stream_ref:
+        print(json.dumps(stream_reference(torch)), flush=True)
         return
 
     # ---- data: one host-quantized weight set, cloned on the device -------

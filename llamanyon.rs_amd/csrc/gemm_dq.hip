@@ -24,7 +24,15 @@
 
 namespace {
 
-constexpr size_t kChunkTarget = size_t(128) << 20;  // bf16 bytes of weights per chunk
+// bf16 bytes of weights per chunk (tuning override: SWAMP_DQ_CHUNK_MB)
+size_t chunk_target() {
+  static const size_t t = [] {
+    const char *e = std::getenv("SWAMP_DQ_CHUNK_MB");
+    const long v = e ? std::atol(e) : 0;
+    return size_t(v >= 16 && v <= 4096 ? v : 128) << 20;
+  }();
+  return t;
+}
 constexpr size_t kLtWorkspace = size_t(32) << 20;   // hipBLASLt workspace offered
 constexpr int kLtCandidates = 16;                    // heuristic candidates measured per shape
 
@@ -54,12 +62,12 @@ LtState &lt_state(int dev) {
   return st[dev & 63];
 }
 
-// Rows per chunk: whole 256-row tiles, at most about kChunkTarget bytes of
+// Rows per chunk: whole 256-row tiles, at most about chunk_target() bytes of
 // bf16.  (Chunks dequantized on a second stream beside the previous chunk's
 // GEMM measured slower: two smaller GEMMs lose more than the overlap wins.)
 int chunk_rows(int n_rows, int n_cols) {
   const size_t total = size_t(n_rows) * size_t(n_cols) * 2;
-  const int chunks = int(std::max<size_t>(1, (total + kChunkTarget - 1) / kChunkTarget));
+  const int chunks = int(std::max<size_t>(1, (total + chunk_target() - 1) / chunk_target()));
   int r = (n_rows + chunks - 1) / chunks;
   r = (r + 255) / 256 * 256;
   return std::min(r, n_rows);

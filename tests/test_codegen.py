@@ -34,10 +34,10 @@ def _asm(tu, out):
         return f.read().split("\n")
 
 
-def _kernels(lines):
+def _kernels(lines, name=r"11gemv_kernel"):
     cur, body = None, []
     for line in lines:
-        m = re.match(r"^(_ZN12_GLOBAL__N_111gemv_kernel\w+):", line)
+        m = re.match(r"^(_ZN12_GLOBAL__N_1" + name + r"\w+):", line)
         if m:
             cur, body = m.group(1), []
             continue
@@ -192,4 +192,19 @@ def test_staged_x_wait_counts_match_emitted_loads(asm):
                 bad.append((tu, name, w))
     # every one-item-per-lane instantiation stages x: plain, RMSNorm, SwiGLU
     assert checked >= 250, checked
+    assert not bad, bad[:5]
+
+
+def test_two_token_gemv_wait_counts_match_emitted_loads(asm):
+    """The two-token GEMV waits for its x DMA by counting the first tile's
+    loads issued after it: that count must be the loads emitted, in every
+    instantiation (4 dtypes x rows per tile x waves per row)."""
+    checked, bad = 0, []
+    for name, body in _kernels(asm["gemv_tokens.hip"], r"15gemv_tok_kernel"):
+        w = _staged_wait(body)
+        assert w is not None, name
+        checked += 1
+        if w[0] != w[1]:
+            bad.append((name, w))
+    assert checked >= 28, checked
     assert not bad, bad[:5]

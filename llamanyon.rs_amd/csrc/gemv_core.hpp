@@ -996,6 +996,15 @@ int waves_per_cu_for(uint32_t dt, int n_cols, int total_rows, bool x32) {
   if (tuning().waves_per_cu) return tuning().waves_per_cu;
   if (!x32) return 4;
   if (n_cols > 4096) return 8;
+  // Q4_0 / Q4_K rows of at most 4096 weights, at least 16 four-row tiles
+  // per wave at 4 waves per CU (the 8B lm_head, 128256 rows): 4 waves with
+  // 4-row tiles stream faster than 8 with 2-row tiles (bench.py decode step,
+  // SWAMP_GEMV_WAVES_PER_CU=4 SWAMP_GEMV_ROWS=4 against the default: Q4_0
+  // lm_head 49.9 against 51.5 us); shorter matrices lose (gate_up 13.8
+  // against 12.6 us), their waves get too few tiles
+  if ((dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) &&
+      long(total_rows) >= 64L * 4 * swamp::device_info().num_cus)
+    return 4;
   if ((dt == SWAMP_Q4_0 || dt == SWAMP_Q4_K) && total_rows >= 6144) return 8;
   if (dt == SWAMP_Q6_K && total_rows >= 16384) return 8;
   return 4;

@@ -19,7 +19,8 @@
 //    64-weight item by a power of two, rounded to fp16 (2^-11 relative),
 //    the magic offsets removed with the matching sums of the same x.  The
 //    fragments of both tokens stay in registers (2 x 35 VGPRs); the kernel
-//    runs two waves per SIMD with up to 256 VGPRs each.
+//    is built for up to 256 VGPRs per wave and launched with one wave per
+//    SIMD (two for Q6_K).
 //  * Tiles of 1 or 2 rows, one item per lane, 1..8 waves per row (rows of
 //    up to 512 items, n_cols <= 32768), row sets sharing x as in the decode
 //    GEMV; the next tile's weights are in flight while the current one is
@@ -160,8 +161,14 @@ int launch_tok(const void *d_w, const float *d_x, float *d_y, int n_tok, int n_r
   const int ipr = n_cols / 64;
   const int n_tiles = (n_rows + kRows - 1) / kRows;
   const int cus = swamp::device_info().num_cus;
-  // two waves per SIMD: 8 waves per CU
-  int grid = cus * std::max(1, 8 / (kWaves * kSets));
+  // Waves per CU: 4 (one per SIMD) for Q4_0 / Q4_K / Q8_0: on the 8B shapes
+  // at 2 tokens (Q4_K layer, Q8_0 lm_head) 137.2 us against 142.7 with 8
+  // per CU (lm_head 93.1 against 97.7, qkv 6.6 against 7.5, o_proj 5.6
+  // against 6.7; gate_up alone is slower, 19.1 against 17.7).  8 for Q6_K,
+  // whose heavier decode needs a second wave per SIMD (its 8B lm_head:
+  // 114 us on 4 waves per CU against 88 on 8).
+  constexpr int kWavesPerCu = DT == SWAMP_Q6_K ? 8 : 4;
+  int grid = cus * std::max(1, kWavesPerCu / (kWaves * kSets));
   const int need = (n_tiles + kSets - 1) / kSets;
   if (grid > need) grid = need;
   gemv_tok_kernel<DT, NT, kRows, kWaves, kSets><<<grid, 64 * kWaves * kSets, 0, s>>>(
@@ -182,8 +189,8 @@ int launch_tok_rows(const void *d_w, const float *d_x, float *d_y, int n_tok, in
   return launch_tok<DT, NT, kRows, 8, 1>(d_w, d_x, d_y, n_tok, n_rows, n_cols, s);
 }
 
-// Rows per tile: 2 when every wave of the grid gets at least one 2-row tile
-// (Q6_K 1, as in the decode GEMV).
+// Rows per tile: 2 when every row set of the grid (4 waves per CU) gets at
+// least two 2-row tiles (Q6_K, on 8 waves per CU, 1 as in the decode GEMV).
 template <int DT, int NT>
 int launch_tok_dt(const void *d_w, const float *d_x, float *d_y, int n_tok, int n_rows,
                   int n_cols, hipStream_t s) {

@@ -189,14 +189,16 @@ int launch_tok_rows(const void *d_w, const float *d_x, float *d_y, int n_tok, in
   return launch_tok<DT, NT, kRows, 8, 1>(d_w, d_x, d_y, n_tok, n_rows, n_cols, s);
 }
 
-// Rows per tile: 2 when every row set of the grid (4 waves per CU) gets at
-// least two 2-row tiles (Q6_K, on 8 waves per CU, 1 as in the decode GEMV).
+// Rows per tile: 2 when every row set of the grid gets at least two 2-row
+// tiles (counted at 8 waves per CU); Q6_K only from 16384 rows, else 1.
 template <int DT, int NT>
 int launch_tok_dt(const void *d_w, const float *d_x, float *d_y, int n_tok, int n_rows,
                   int n_cols, hipStream_t s) {
   const int cus = swamp::device_info().num_cus;
   const long slots = long(cus) * std::max(1, 8 / waves_for(n_cols / 64));
-  if constexpr (DT != SWAMP_Q6_K) {
+  // Q6_K from 16384 rows only (8B gate_up and lm_head faster with 2-row
+  // tiles, the shorter qkv, o_proj and down slower)
+  if (DT != SWAMP_Q6_K || n_rows >= 16384) {
     if (long(n_rows) / 2 >= slots)
       return launch_tok_rows<DT, NT, 2>(d_w, d_x, d_y, n_tok, n_rows, n_cols, s);
   }

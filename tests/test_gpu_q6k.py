@@ -208,7 +208,7 @@ def _batched_err(pkg, orc, raw, xs, y, rows, cols, sel=None):
 # three passes (32 + 32 + 6), one block pair per row (512); two tokens run
 # the GEMV over both; one token and rows of an odd number of blocks (768)
 # run the decode GEMV per token
-@pytest.mark.parametrize("n_tok,rows,cols", [(1, 300, 4096), (2, 77, 512), (5, 1000, 4096),
+@pytest.mark.parametrize("n_tok,rows,cols", [(1, 300, 4096), (2, 77, 512), (2, 16385, 512), (5, 1000, 4096),
                                              (16, 1024, 14336), (17, 64, 14336),
                                              (32, 2000, 4096), (32, 100, 14336),
                                              (70, 256, 2048), (3, 40, 768), (5, 33, 512),
@@ -239,7 +239,7 @@ def test_q6k_batched(pkg, orc, torch_dev, errlog, n_tok, rows, cols):
     assert e.value.code == pkg.EDTYPE
 
 
-@pytest.mark.parametrize("n_tok", [4, 16, 32])
+@pytest.mark.parametrize("n_tok", [2, 4, 16, 32])
 def test_q6k_batched_lm_head_subsets(pkg, orc, torch_dev, errlog, n_tok):
     """Llama-3 8B lm_head, 128256 x 4096 Q6_K (as Q4_K_M files keep it), in
     one pass: the oracle on three row ranges; every token's rows equal the

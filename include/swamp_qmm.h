@@ -80,8 +80,8 @@ SWAMP_API int swamp_qdequant(uint32_t dtype, const void *d_raw, size_t raw_len,
                    float *d_dst, size_t n, void *stream);
 
 /* No counterpart in the reference: the bf16 form of swamp_qdequant, the
- * pass the prefill GEMM's dequantize-once route runs before its bf16
- * library GEMM, exported so that its output can be checked bit for bit and
+ * pass the prefill GEMM's dequantize-once route runs before its plain bf16
+ * GEMM, exported so that its output can be checked bit for bit and
  * for callers that feed their own bf16 GEMM.  Writes n bf16 values (raw
  * bits, uint16) to d_dst: each the swamp_qdequant value rounded to nearest
  * even (NaN stays NaN).  dtype Q4_0, Q8_0 (n a multiple of 32, d_raw 4-byte
@@ -213,30 +213,34 @@ SWAMP_API int swamp_qgemv_batched(uint32_t dtype, const void *d_w, size_t w_len,
  *     of 128.
  * dtype Q4_0, Q8_0, Q4_K or Q6_K (Q6_K with bf16 x only); bf16 x needs
  * n_cols a multiple of 64.
- * Below 1024 tokens (bf16 x) the fused kernel dequantizes weight tiles in
- * registers to bf16; when the tiles do not fill the GPU, K is split across
+ * With bf16 x the fused kernel dequantizes weight tiles in registers to
+ * bf16 (every tile reads the quantized blocks: 0.56-1.06 bytes per
+ * weight); when the tiles do not fill the GPU, K is split across
  * workgroups whose partial tiles go to scratch and are summed in piece
- * order by a second kernel (deterministic).  From 1024 tokens (matrices of
- * at least 1024 x 1024), and for Q6_K at any length, the weights are
+ * order by a second kernel (deterministic).  For Q6_K at any length, and
+ * from 1024 tokens when 256 x 256 tiles would fill more than half but not
+ * all of the CUs (e.g. 2048 tokens x 6144 rows), the weights are instead
  * dequantized once per call to bf16 in scratch (row chunks of at most
- * 128 MB; the same bf16 values) and each chunk is multiplied by a hipBLASLt
- * bf16 GEMM with fp32 accumulation; when that scratch cannot be had the
- * fused kernel runs (Q6_K: SWAMP_EWORKSPACE).  The first such call of a
- * shape on a device measures the library's candidate algorithms on its
- * stream and keeps the fastest (a one-time step that waits for the stream;
- * skipped under graph capture and with SWAMP_GEMM_TUNE=0); the choice may
- * differ between processes, and with it the order of the fp32 sums. */
+ * 512 MB; the same bf16 values) and each chunk runs through this library's
+ * plain bf16 x bf16 -> fp32 MFMA GEMM, whose 192- and 128-row tiles fill
+ * the CUs; when that scratch cannot be had the fused kernel runs (Q6_K:
+ * SWAMP_EWORKSPACE).  Both routes sum in a fixed order: repeated calls
+ * give the same bits. */
 SWAMP_API int swamp_qgemm(uint32_t dtype, const void *d_w, size_t w_len,
                 const void *d_x, uint32_t x_type, float *d_y, int m,
                 int n_rows, int n_cols, void *stream);
 
 /* Scratch.  swamp_qgemv_batched and swamp_qgemm need scratch memory for
- * some shapes (the partial sums of K split across workgroups, and the bf16
- * copy of x of a batch of more than 64 tokens).  The library keeps one
- * buffer per (device, stream) for it (hipStreamPerThread: per host thread
- * too), allocated on first use and replaced when a call needs more, both
+ * some shapes (the partial sums of K split across workgroups, the bf16
+ * copy of x of a batch of more than 64 tokens, and the bf16 weight chunk
+ * of the GEMM's dequantize-once route).  The library keeps one buffer per
+ * (device, stream) for it (hipStreamPerThread: per host thread too),
+ * allocated on first use and replaced when a call needs more, both
  * stream-ordered on that stream (hipMallocAsync / hipFreeAsync): no call
- * synchronizes the host.  While the stream is being captured into a graph
+ * synchronizes the host.  A buffer that a call under graph capture used is
+ * never freed (the graph's replays write it): when a later call needs
+ * more, it is kept until the process ends and a new one replaces it for
+ * the stream's eager calls.  While the stream is being captured into a graph
  * nothing is allocated: a call that needs more than the stream's buffer
  * holds takes the path without scratch (split pieces added with float
  * atomics into y cleared by a kernel, which is not bit-reproducible; more

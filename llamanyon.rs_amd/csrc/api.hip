@@ -127,33 +127,44 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
     std::thread::id tid;  // for hipStreamPerThread, one stream per host thread
     void *p;
     size_t bytes;
+    bool captured;  // handed out while s was being captured: a graph may hold it
   };
   static std::mutex mu;
   static std::vector<Entry> cache;
+  static std::vector<void *> retired;  // replaced buffers a graph may hold (never freed)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   const std::thread::id tid =
       s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return nullptr;
+  const bool capturing = st != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> lock(mu);
   Entry *e = nullptr;
   for (Entry &c : cache)
     if (c.dev == dev && c.s == s && c.tid == tid) e = &c;
-  if (e && e->bytes >= bytes) return e->p;
+  if (e && e->bytes >= bytes) {
+    e->captured = e->captured || capturing;
+    return e->p;
+  }
   // a (larger) buffer is needed: never while the stream is being captured
-  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
-    return nullptr;
+  if (capturing) return nullptr;
   void *p = nullptr;
   if (hipMallocAsync(&p, bytes, s) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
   if (e) {
-    (void)hipFreeAsync(e->p, s);  // after the work already queued on s
+    // A buffer a captured call used stays allocated until the process ends
+    // (the graph's replays write it); any other is released after the work
+    // already queued on s.
+    if (e->captured) retired.push_back(e->p);
+    else (void)hipFreeAsync(e->p, s);
     e->p = p;
     e->bytes = bytes;
+    e->captured = false;
   } else {
-    cache.push_back(Entry{dev, s, tid, p, bytes});
+    cache.push_back(Entry{dev, s, tid, p, bytes, false});
   }
   return p;
 }

@@ -30,9 +30,10 @@
 //    loads stay in flight.
 //  * Dequantization is q * s + o rounded once in fp32 by an fma (exact up
 //    to that rounding) and then to bf16: the same B values as the
-//    dequantization kernels produce, rounded to bf16.  Nibbles are masked
-//    in place (w & 0x0F0F0F0F, w & 0xF0F0F0F0) and read by the byte
-//    converts; the high nibbles come out as 16q and take s / 16 (exact).
+//    dequantization kernels produce, rounded to bf16.  Nibble codes reach
+//    fp32 two per instruction through gfx950's scaled fp8 convert (a byte
+//    below 16 read as E4M3 is the integer times 2^-9; the scale operand
+//    supplies 2^9): low nibbles masked in place, high ones shifted down.
 //  * Tile order: groups of 4 token tiles, consecutive tiles walking the
 //    weight columns of a group; workgroup ids are remapped so each XCD
 //    (ids i, i+8, ...) runs a contiguous run of that order.  A round of an
@@ -100,20 +101,30 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, ui
                                            voff, soff, 0, 0);
 }
 
-// Eight weights from the four bytes of w as 16q_hi / q_lo pairs: byte p
-// holds elements 2p (low nibble, scale s) and 2p + 1 (high nibble, read
-// as 16 q with scale s16 = s / 16); value q * s + o.  The empty asm keeps
-// the masked words opaque, so the byte converts read them directly
-// instead of re-extracting each nibble.
-__device__ __forceinline__ u32x4v_t deq_pairs(uint32_t w, float s, float s16, float o) {
-  uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
-  asm("" : "+v"(lo), "+v"(hi));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two nibble codes c0, c1 (bytes 2 sel, 2 sel + 1 of a word whose bytes are
+// all below 16) as fp32: a byte below 16 read as OCP E4M3 is the integer
+// times 2^-9 (the denormals run on linearly into the first binade), and the
+// convert's scale operand, of which only the power of two counts, supplies
+// 2^9 -- exact, two codes per instruction.
+template <bool kSel>
+__device__ __forceinline__ f32x2_t nib_pair(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 512.0f, kSel);
+}
+
+// Eight weights from the four bytes of w: byte p holds elements 2p (low
+// nibble) and 2p + 1 (high nibble); value q * s + o, one fp32 rounding,
+// then bf16.
+__device__ __forceinline__ u32x4v_t deq_pairs(uint32_t w, float s, float o) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  const f32x2_t l0 = nib_pair<false>(lo), l1 = nib_pair<true>(lo);
+  const f32x2_t h0 = nib_pair<false>(hi), h1 = nib_pair<true>(hi);
   u32x4v_t out;
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    const float a = float((lo >> (8 * p)) & 0xFFu), b = float((hi >> (8 * p)) & 0xFFu);
-    out[p] = pack_bf16(__builtin_fmaf(a, s, o), __builtin_fmaf(b, s16, o));
-  }
+  out[0] = pack_bf16(__builtin_fmaf(l0[0], s, o), __builtin_fmaf(h0[0], s, o));
+  out[1] = pack_bf16(__builtin_fmaf(l0[1], s, o), __builtin_fmaf(h0[1], s, o));
+  out[2] = pack_bf16(__builtin_fmaf(l1[0], s, o), __builtin_fmaf(h1[0], s, o));
+  out[3] = pack_bf16(__builtin_fmaf(l1[1], s, o), __builtin_fmaf(h1[1], s, o));
   return out;
 }
 
@@ -129,6 +140,18 @@ __device__ __forceinline__ u32x4v_t deq_bytes(uint32_t w0, uint32_t w1, float s,
     out[2 + p] = pack_bf16(__builtin_fmaf(float((w1 >> (16 * p)) & 0xFFu), s, o),
                            __builtin_fmaf(float((w1 >> (16 * p + 8)) & 0xFFu), s, o));
   }
+  return out;
+}
+
+// The same for bytes that are all below 16 (nibble codes), through nib_pair.
+__device__ __forceinline__ u32x4v_t deq_nibbles(uint32_t w0, uint32_t w1, float s, float o) {
+  const f32x2_t a = nib_pair<false>(w0), b = nib_pair<true>(w0);
+  const f32x2_t c = nib_pair<false>(w1), d = nib_pair<true>(w1);
+  u32x4v_t out;
+  out[0] = pack_bf16(__builtin_fmaf(a[0], s, o), __builtin_fmaf(a[1], s, o));
+  out[1] = pack_bf16(__builtin_fmaf(b[0], s, o), __builtin_fmaf(b[1], s, o));
+  out[2] = pack_bf16(__builtin_fmaf(c[0], s, o), __builtin_fmaf(c[1], s, o));
+  out[3] = pack_bf16(__builtin_fmaf(d[0], s, o), __builtin_fmaf(d[1], s, o));
   return out;
 }
 
@@ -190,7 +213,7 @@ __device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
     const uint32_t hi0 = S < 3 ? r.d[S + 2] : r.d[0];
     const uint32_t w = __builtin_amdgcn_alignbyte(hi0, r.d[S + 1], sh);
     const float d = swamp::f16_bits_to_f32(h ? r.d[0] >> 16 : r.d[1] & 0xFFFFu);
-    return deq_pairs(w, d, 0.0625f * d, -8.0f * d);
+    return deq_pairs(w, d, -8.0f * d);
   } else if constexpr (DT == SWAMP_Q8_0) {
     // block h: d, then 32 int8; chunk S is quant bytes 8S .. 8S + 7.  Block
     // 0's quants start at byte 2 of d[1] (bytes 32, 33 sit in d[0]); block
@@ -218,9 +241,9 @@ __device__ __forceinline__ u32x4v_t b_frag(const WItem<DT> &r, bool h) {
     (void)h;
     constexpr int t = 2 * (S & 1);
     const uint32_t w0 = r.q[t], w1 = r.q[t + 1];
-    // low nibbles: bytes of w & 0x0F0F0F0F; high: w & 0xF0F0F0F0 (16 q)
-    constexpr uint32_t mask = hb ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    return deq_bytes(w0 & mask, w1 & mask, hb ? 0.0625f * sc : sc, o);
+    // low nibbles: bytes of w & 0x0F0F0F0F; high: of (w >> 4) & 0x0F0F0F0F
+    const uint32_t a0 = hb ? w0 >> 4 : w0, a1 = hb ? w1 >> 4 : w1;
+    return deq_nibbles(a0 & 0x0F0F0F0Fu, a1 & 0x0F0F0F0Fu, sc, o);
   }
 }
 
@@ -699,7 +722,7 @@ size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_ro
   if (x_type == SWAMP_Q8_0) return swamp_gemm_i8_scratch_bytes(dtype, m, n_rows, n_cols);
   if (x_type != SWAMP_BF16 || n_cols % kBK != 0) return 0;
   if (swamp_gemm_dq_route(dtype, m, n_rows, n_cols)) {
-    const size_t dq = swamp_gemm_dq_scratch_bytes(n_rows, n_cols);
+    const size_t dq = swamp_gemm_dq_scratch_bytes(m, n_rows, n_cols);
     if (dq <= limit || dtype == SWAMP_Q6_K) return dq;
   }
   switch (dtype) {
@@ -723,7 +746,7 @@ int swamp_launch_gemm(uint32_t dtype, const void *d_w, const void *d_x, uint32_t
   // long prompts: dequantize once to bf16 and run a plain bf16 GEMM, when
   // the scratch for it is there (else the fused kernel below)
   if (swamp_gemm_dq_route(dtype, m, n_rows, n_cols) &&
-      sc.cap - sc.used >= swamp_gemm_dq_scratch_bytes(n_rows, n_cols)) {
+      sc.cap - sc.used >= swamp_gemm_dq_scratch_bytes(m, n_rows, n_cols)) {
     const size_t used = sc.used;
     const int rc = swamp_launch_gemm_dq(dtype, d_w, d_x, d_y, m, n_rows, n_cols, sc, s);
     if (rc != kDqUnavailable) return rc;

@@ -175,13 +175,13 @@ size_t swamp_batched_scratch_bytes(uint32_t dtype, int n_tok, int n_rows, int n_
 // limit: scratch the caller can offer; a route that needs more is not taken.
 size_t swamp_gemm_scratch_bytes(uint32_t dtype, uint32_t x_type, int m, int n_rows, int n_cols,
                                 size_t limit = SIZE_MAX);
-// The bf16 GEMM's dequantize-once route (gemm_dq.hip): whether a shape takes
-// it, its scratch, and the launcher, which returns kDqUnavailable, having
-// launched nothing, when the scratch or a library plan for the shape is
-// missing (the caller then runs the fused kernel).
+// The bf16 GEMM's dequantize-once route (gemm_dq.hip, gemm_bb.hip): whether
+// a shape takes it, its scratch, and the launcher, which returns
+// kDqUnavailable, having launched nothing, when the scratch is missing (the
+// caller then runs the fused kernel).
 constexpr int kDqUnavailable = 1;
 bool swamp_gemm_dq_route(uint32_t dtype, int m, int n_rows, int n_cols);
-size_t swamp_gemm_dq_scratch_bytes(int n_rows, int n_cols);
+size_t swamp_gemm_dq_scratch_bytes(int m, int n_rows, int n_cols);
 int swamp_launch_gemm_dq(uint32_t dtype, const void *d_w, const void *d_x, float *d_y, int m,
                          int n_rows, int n_cols, swamp::Scratch &sc, hipStream_t s);
 int swamp_launch_gemv_batched(uint32_t dtype, const void *d_w,

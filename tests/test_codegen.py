@@ -136,7 +136,7 @@ def _gemm_wait_problems(body):
 
 _TUS = ["api.hip", "device.hip", "dequant.hip", "gemv.hip", "gemv_fused.hip", "gemv_tokens.hip",
         "gemv_batched.hip",
-        "gemm.hip", "gemm_dq.hip",
+        "gemm.hip", "gemm_dq.hip", "gemm_bb.hip",
         "gemm_i8.hip", "gguf.hip", "producers.hip"]
 
 

@@ -11,7 +11,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K, F32, BF16 = 2, 8, 12, 0, 30
+Q4_0, Q8_0, Q4_K, Q6_K, F32, BF16 = 2, 8, 12, 14, 0, 30
 TOL = 1e-3
 HIP_STREAM_PER_THREAD = 2  # hipStreamPerThread
 
@@ -57,8 +57,12 @@ def test_workspace_queries(pkg, torch_dev):
     assert L.swamp_qgemm_workspace(Q4_0, Q8_0, 64, 512, 4096) > 0
     # a full round of tiles on the fused kernel: no split
     assert L.swamp_qgemm_workspace(Q4_0, BF16, 512, 28672, 4096) == 0
-    # a long prompt: dequantize-once route (bf16 weight chunk + library workspace)
-    assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 28672, 4096) > 0
+    # full rounds plus a last round of half tiles: no split either
+    assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 28672, 4096) == 0
+    # between half a round and one round of full tiles at 2048 tokens, and Q6_K:
+    # the dequantize-once route (a bf16 weight chunk)
+    assert L.swamp_qgemm_workspace(Q4_0, BF16, 2048, 6144, 4096) >= 6144 * 4096 * 2
+    assert L.swamp_qgemm_workspace(Q6_K, BF16, 64, 512, 4096) >= 512 * 4096 * 2
     # small batch: K groups on a short matrix (also with token groups, 40
     # tokens); more than 64 tokens: bf16 x for the GEMM
     assert L.swamp_qgemv_batched_workspace(Q4_K, 16, 4096, 14336, 0) > 0
@@ -191,6 +195,48 @@ def test_graph_capture_with_reserved_scratch(pkg, torch_dev):
         for c in calls:
             _run(pkg, c, cs.cuda_stream)
     for rep in range(3):
+        for c in calls:
+            c["d_y"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(calls, eager):
+            assert np.array_equal(c["d_y"].cpu().numpy().view(np.uint32), e.view(np.uint32)), rep
+
+
+def test_graph_keeps_scratch_after_larger_eager_call(pkg, torch_dev):
+    """Reserve, capture, then an eager call on the same stream that needs a
+    larger buffer: the stream's buffer is replaced, but the one the graph
+    holds stays allocated, and every replay still gives the eager bits."""
+    torch = torch_dev
+    cs = torch.cuda.Stream()
+    calls = _calls(pkg, torch, mid=3)
+    need = max(_need(pkg, c) for c in calls)
+    print("[gpu case] graph replay after a larger eager call", flush=True)
+    with torch.cuda.stream(cs):
+        pkg.workspace_reserve(cs.cuda_stream, need)
+        for c in calls:
+            _run(pkg, c, cs.cuda_stream)
+    torch.cuda.synchronize()
+    eager = [c["d_y"].cpu().numpy().copy() for c in calls]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for c in calls:
+            _run(pkg, c, cs.cuda_stream)
+    # a Q6_K prefill: the dequantize-once route, whose bf16 weight chunk is
+    # far larger than the reservation
+    rows, cols, n = 1024, 4096, 64
+    big = pkg.gpu_lib().swamp_qgemm_workspace(Q6_K, BF16, n, rows, cols)
+    assert big > need
+    raw = weights(pkg, Q6_K, rows, cols, mid=7)
+    d_w = torch.from_numpy(raw).cuda()
+    d_x = torch.from_numpy(bf16(pkg, acts(pkg, n, cols, mid=7))[0].view(np.int16)).cuda()
+    d_y = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    for rep in range(3):
+        with torch.cuda.stream(cs):
+            pkg.qgemm(Q6_K, d_w.data_ptr(), raw.size, d_x.data_ptr(), BF16, d_y.data_ptr(), n,
+                      rows, cols, cs.cuda_stream)
+        torch.cuda.synchronize()
         for c in calls:
             c["d_y"].fill_(float("nan"))
         torch.cuda.synchronize()

@@ -287,7 +287,7 @@ int launch_bb(const uint16_t *w, const uint16_t *x, float *y, int m, int n, int 
 }
 
 #ifndef BB_FULL
-#define BB_FULL 4, 2, 2, 4
+#define BB_FULL 4, 4, 2, 2
 #endif
 #ifndef BB_HALF
 #define BB_HALF 2, 4, 2, 2

@@ -178,6 +178,65 @@ def test_gemm_wait_counts_match_emitted_loads(asm):
     assert not bad, bad
 
 
+def _bb_wait_problems(body):
+    """Checks the plain bf16 GEMM's hand-counted waits (gemm_bb.hip).  The
+    prologue issues three steps of P activation/weight DMAs and waits with
+    vmcnt(2 P) (the first step landed).  Each trip of the K loop is one
+    step: it issues P DMAs, D of them before its one barrier, and the wait
+    before that barrier must be P + D (the previous step's DMAs and this
+    step's first D stay in flight: the step after the current one has
+    landed).  No other vector-memory access may sit in the loop (a flat
+    access to LDS would also count), and no vmcnt(0)."""
+    bars = [i for i, l in enumerate(body) if l.strip().startswith("s_barrier")]
+
+    def wait_before(b):
+        for j in range(b - 1, max(b - 4, -1), -1):
+            m = re.search(r"vmcnt\((\d+)\)", body[j])
+            if m:
+                return int(m.group(1))
+        return None
+
+    probs = []
+    pro = [l for l in body[:bars[0]] if _VMEM.search(l)]
+    if not pro or not all(l.rstrip().endswith(" lds") for l in pro) or len(pro) % 3:
+        return ["prologue is not three steps of DMAs: %d loads" % len(pro)]
+    p = len(pro) // 3
+    if wait_before(bars[0]) != 2 * p:
+        probs.append("prologue wait %s != %d" % (wait_before(bars[0]), 2 * p))
+    head = [i for i, l in enumerate(body) if "Loop Header" in l]
+    if not head:
+        return probs + ["no K loop found"]
+    label = body[head[0]].split(":")[0]
+    back = [i for i, l in enumerate(body)
+            if re.match(r"\s+s_(c)?branch", l) and re.search(re.escape(label) + r"\b", l)]
+    if not back:
+        return probs + ["no K loop back-branch"]
+    lo, hi = head[0], back[-1]
+    loop_bars = [b for b in bars if lo < b < hi]
+    if len(loop_bars) != 1:
+        return probs + ["%d barriers in the K loop, expected 1" % len(loop_bars)]
+    mem = [i for i in range(lo, hi + 1) if re.search(r"\b(buffer_|global_|flat_)", body[i])]
+    if any(not body[i].rstrip().endswith(" lds") for i in mem):
+        probs.append("a vector-memory access other than a DMA in the K loop")
+    if len(mem) != p:
+        probs.append("%d DMAs in the K loop, expected %d" % (len(mem), p))
+    d = sum(1 for i in mem if i < loop_bars[0])
+    if wait_before(loop_bars[0]) != p + d:
+        probs.append("loop wait %s != %d + %d" % (wait_before(loop_bars[0]), p, d))
+    if any("vmcnt(0)" in l for l in body[lo:hi + 1]):
+        probs.append("vmcnt(0) inside the K loop")
+    return probs
+
+
+def test_bb_gemm_wait_counts_match_emitted_loads(asm):
+    lines = asm["gemm_bb.hip"]
+    kernels = list(_kernels(lines, r"14gemm_bb_kernel"))
+    # full, 192-row, 128-row and half tiles
+    assert len(kernels) == 4, [k for k, _ in kernels]
+    bad = [(name, p) for name, body in kernels for p in [_bb_wait_problems(body)] if p]
+    assert not bad, bad
+
+
 def test_staged_x_wait_counts_match_emitted_loads(asm):
     tus = ["gemv.hip", "gemv_fused.hip"]
     asms = [asm[t] for t in tus]

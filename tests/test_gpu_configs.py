@@ -233,27 +233,34 @@ def _gemm(pkg, orc, torch, W, dtype, sigma, rows, cols, m, x_type, mid):
 PREFILL8B = ["gate_up", "down", "qkv"]
 
 
-@pytest.mark.parametrize("x_type", [BF16, Q8_0], ids=["bf16", "q8_0"])
+@pytest.mark.parametrize("route", ["fused", "dq", "q8_0"])
 @pytest.mark.parametrize("m", [512, 2048])
 @pytest.mark.parametrize("name", PREFILL8B)
-def test_config4_prefill(pkg, orc, torch_dev, W, errlog, name, m, x_type):
+def test_config4_prefill(pkg, orc, torch_dev, W, errlog, monkeypatch, name, m, route):
     """Config 4: Q4_0 prefill GEMM at the 8B FFN and attention shapes, bf16
-    x on the bf16 matrix cores and Q8_0 x on the int8 matrix cores."""
+    x on the bf16 matrix cores (both routes, forced per call: the fused
+    kernel and the dequantize-once plain GEMM) and Q8_0 x on the int8
+    matrix cores."""
     rows, cols = LLAMA8B[name]
-    print(f"[gpu case] config4 prefill {name} m {m} x_type {x_type}", flush=True)
+    x_type = Q8_0 if route == "q8_0" else BF16
+    if x_type == BF16:
+        monkeypatch.setenv("SWAMP_GEMM_ROUTE", route)
+    print(f"[gpu case] config4 prefill {name} m {m} route {route}", flush=True)
     err = _gemm(pkg, orc, torch_dev, W, Q4_0, 0.02, rows, cols, m, x_type, mid=rows)
     path = "gemm_bf16" if x_type == BF16 else "gemm_i8"
-    errlog(f"prefill 8b {name} m={m} {'bf16' if x_type == BF16 else 'q8_0'}", err, path=path)
+    errlog(f"prefill 8b {name} m={m} {route}", err, path=path)
     assert err <= min(TOL, BOUND[path])
 
 
+@pytest.mark.parametrize("route", ["fused", "dq"])
 @pytest.mark.parametrize("name", list(LLAMA70B))
-def test_config5_prefill(pkg, orc, torch_dev, W, errlog, name):
+def test_config5_prefill(pkg, orc, torch_dev, W, errlog, monkeypatch, name, route):
     """Config 5: the 4096-token bf16 prefill GEMM at the 70B shapes (Q4_K,
-    Q8_0 lm_head)."""
+    Q8_0 lm_head), on both routes (forced per call)."""
     rows, cols = LLAMA70B[name]
     dtype = Q8_0 if name == "lm_head" else Q4_K
-    print(f"[gpu case] config5 prefill {name} m 4096", flush=True)
+    monkeypatch.setenv("SWAMP_GEMM_ROUTE", route)
+    print(f"[gpu case] config5 prefill {name} m 4096 route {route}", flush=True)
     err = _gemm(pkg, orc, torch_dev, W, dtype, 0.015, rows, cols, 4096, BF16, mid=rows)
-    errlog(f"prefill 70b {name} m=4096 bf16", err, path="gemm_bf16")
+    errlog(f"prefill 70b {name} m=4096 bf16 {route}", err, path="gemm_bf16")
     assert err <= min(TOL, BOUND["gemm_bf16"])

@@ -405,25 +405,32 @@ def test_gemm_bf16_parity(pkg, orc, torch_dev, dtype, m, rows, cols):
     assert orc.normalized_error(y[toks], ref, deq, x_fed[toks]) <= TOL
 
 
-# Every work decomposition of the bf16 GEMM (256-token x 256-row tiles on
+# Every work decomposition of the bf16 GEMM, on both routes (forced per
+# call with SWAMP_GEMM_ROUTE).  Fused kernel (256-token x 256-row tiles on
 # the CUs of one MI355X): complete rounds of full tiles; full tiles plus a
 # last round of 128-token half tiles (ragged tokens and rows: the second
 # half of the short last token tile is empty); one partial round of full
 # tiles; at most half a round: full tiles in 2 and in 5 K pieces summed
-# through the workspace; short K (8 steps): half tiles.
+# through the workspace; short K (8 steps): half tiles; at most 64 tokens:
+# quarter tiles, split along K.  Dequantize-once route (plain bf16 GEMM):
+# full rounds plus a last round of half tiles (1900 x 28572), 192-row tiles
+# (2048 x 6144), 128-row tiles (2048 x 4096 x 14336, 100 x 600), 128-row
+# tiles split along K into 8 pieces (64 x 4096 x 14336) and 2 (1 x 600).
 DECOMP_CASES = [(2048, 8192, 4096), (1900, 28572, 4096), (2048, 6144, 4096), (2048, 4096, 14336),
                 (512, 6144, 4096), (100, 600, 512), (48, 28672, 4096), (64, 4096, 14336), (1, 600, 1024)]
 
 
+@pytest.mark.parametrize("route", ["fused", "dq"])
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
 @pytest.mark.parametrize("m,rows,cols", DECOMP_CASES)
-def test_gemm_bf16_decompositions(pkg, orc, torch_dev, dtype, m, rows, cols):
+def test_gemm_bf16_decompositions(pkg, orc, torch_dev, monkeypatch, dtype, m, rows, cols, route):
     torch = torch_dev
+    monkeypatch.setenv("SWAMP_GEMM_ROUTE", route)
     raw = weights(pkg, dtype, rows, cols, mid=rows ^ m)
     x = acts(pkg, m, cols, mid=m ^ cols)
     xb = pkg.to_bf16_bits(x)
     x_fed = (xb.astype(np.uint32) << 16).view(np.float32)
-    say("gemm bf16 decomposition", dtype, m, rows, cols)
+    say("gemm bf16 decomposition", route, dtype, m, rows, cols)
     d_w, d_x = up(torch, raw), up(torch, xb.view(np.int16))
     d_y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
     pkg.qgemm(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), BF16, d_y.data_ptr(), m, rows,

@@ -26,6 +26,15 @@ Also reported (outside the timed steps):
     activations (fraction of the 2.5 PFLOP/s dense bf16 peak) and with
     Q8_0-quantized activations on the int8 MFMA (quantizer included;
     fraction of the 5.0 POP/s dense int8 peak);
+  * small_batch: the Llama-3-8B layer in Q4_K with the lm_head in Q8_0 at
+    1, 4, 8 and 16 tokens (swamp_qgemv, swamp_qgemv_batched), each matrix
+    timed alone and summed (GB/s, fraction of HBM peak, GFLOP/s), with its
+    CPU lines (the reference's fused_gemv_q4k_scalar and batched_scalar,
+    restated in C) at the same thread counts as cpu_baseline;
+  * decode_70b: the Llama-3-70B layer in Q4_K with the lm_head in Q8_0 at
+    batch 1, the same way;
+  * prefill_70b: the 70B gate+up, down and QKV as 4096-token bf16 prefill
+    GEMMs (fraction of the bf16 peak);
   * cpu_baseline: the reference's CPU matmul path (forward_linear fallback:
     dequantize the whole tensor on one thread, then a row-partitioned f32
     dot), restated in C and compiled here with -O3 -march=native
@@ -34,12 +43,13 @@ Also reported (outside the timed steps):
     with the CPU model.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--no-prefill] [--cpu-threads 6,max] [--sweep] [--pmc-probe] [--pmc-gemm]
-                       [--pmc-batched N]
+                       [--no-prefill] [--no-small-batch] [--no-70b] [--cpu-threads 6,max]
+                       [--sweep] [--pmc-probe] [--pmc-gemm] [--pmc-batched N]
 --sweep adds one JSON line per extra workload after the main line: the
-Q4_K small-batch sweep (1/2/4/8/16/17/24/32/64 tokens; 2 as one GEMV, 17-64 in token groups
-of 16) at 8B shapes and the 70B layer
-(decode and 4096-token prefill).  --pmc-probe runs only the dominant kernel
+Q4_K small batch at 2, 17, 24, 32 and 64 tokens (2 as one GEMV, 17-64 in
+token groups of 16) at 8B shapes, the 8B shapes in Q6_K, the activation
+producers, the rest of the 70B prefill and the int8 prefill with Q4_K
+weights.  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
 --pmc-gemm the same for the 2048-token gate+up prefill GEMM; --pmc-batched N
 runs 5 small-batch launches of N tokens per 8B sweep matrix, for counter passes.
@@ -210,15 +220,13 @@ def cpu_baseline(pkg, thread_counts, min_seconds=8.0):
     }
 
 
-def cpu_sweep(pkg, thread_counts, min_seconds=4.0):
-    """CPU lines for the other configurations (opt-in, --sweep), with the
-    same oracle build: the Q4_K scalar GEMV (fused_gemv_q4k_scalar,
-    fused_gemv_q4k.rs:466-508, rows partitioned as linear.rs:28-47) and the
-    Q4_K small batch (batched_scalar, :650-698, rows partitioned as
-    linear.rs:209-236) over the four 8B layer matrices, and the Q4_0
-    prefill as forward_linear per token (linear.rs:68-88 applied to each
-    token: the reference's own batched Q4_0 arm decodes the bytes as Q4_K,
-    linear.rs:358), on a sample of tokens."""
+def cpu_small_batch(pkg, thread_counts, min_seconds=2.0):
+    """CPU lines of the small batch, with the oracle build of cpu_baseline:
+    the Q4_K scalar GEMV (fused_gemv_q4k_scalar, fused_gemv_q4k.rs:466-508,
+    rows partitioned as linear.rs:28-47) at 1 token and the Q4_K small batch
+    (batched_scalar, :650-698, rows partitioned as linear.rs:209-236) at 4,
+    8 and 16 tokens, over the four 8B layer matrices (the lm_head is left
+    out to bound the time); GB/s over their algorithmic bytes."""
     orc, build = _cpu_oracle()
     layer = [(n, r, k) for n, r, k in SWEEP_8B if n != "lm_head"]
     mats = [(pkg.synth_quantized(pkg.Q4_K, SEED ^ 0x900 ^ i, 0.02, r, k), r, k)
@@ -233,6 +241,7 @@ def cpu_sweep(pkg, thread_counts, min_seconds=4.0):
             times.append(time.perf_counter() - t0)
         return float(sum(times) / len(times)), len(times)
 
+    lines = []
     for n_tok in (1, 4, 8, 16):
         xs = [pkg.fill_normal(SEED ^ 0xA00 ^ i, 1.0, n_tok, k) for i, (_, _, k) in enumerate(layer)]
         nbytes = sum(int(r * k * 144 // 256) + n_tok * k * 4 + n_tok * r * 4 for _, r, k in mats)
@@ -247,11 +256,27 @@ def cpu_sweep(pkg, thread_counts, min_seconds=4.0):
             t, reps = timed(fn)
             runs.append({"threads": nt, "GB/s": round(nbytes / t / 1e9, 4),
                          "seconds_per_call": round(t, 4), "reps": reps})
-        print(json.dumps({"cpu_sweep": "llama3-8b Q4_K layer (qkv, o_proj, gate_up, down): "
-                                       + ("fused_gemv_q4k_scalar" if n_tok == 1
-                                          else "batched_scalar"),
-                          "n_tok": n_tok, "alg_bytes": nbytes, "model": cpu_model(),
-                          "build": build, "runs": runs}), flush=True)
+        lines.append({"path": "fused_gemv_q4k_scalar" if n_tok == 1 else "batched_scalar",
+                      "n_tok": n_tok, "alg_bytes": nbytes, "runs": runs})
+    return {"workload": "llama3-8b Q4_K layer (qkv, o_proj, gate_up, down), kind port",
+            "model": cpu_model(), "build": build, "lines": lines}
+
+
+def cpu_sweep(pkg, thread_counts, min_seconds=4.0):
+    """The Q4_0 prefill as forward_linear per token (opt-in, --sweep):
+    linear.rs:68-88 applied to each token (the reference's own batched Q4_0
+    arm decodes the bytes as Q4_K, linear.rs:358), on a sample of tokens."""
+    orc, build = _cpu_oracle()
+
+    def timed(fn):
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 2 or time.perf_counter() - t_start < min_seconds:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(sum(times) / len(times)), len(times)
+
     # Q4_0 prefill semantics: forward_linear per token, on a token sample
     sample = 2
     per = []
@@ -276,15 +301,115 @@ SWEEP_70B = [("qkv", 10240, 8192), ("o_proj", 8192, 8192), ("gate_up", 57344, 81
              ("down", 8192, 28672), ("lm_head", 128256, 8192)]
 
 
+def _timed(torch, stream, fn, reps=20):
+    """Mean time (us) of `reps` back-to-back calls fn(i), after 3 untimed
+    ones and a GPU sleep (so the timed calls do not queue behind them)."""
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(20_000_000)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def _copies(nbytes):
+    """Weight copies rotated per matrix: enough that the matrices cycled
+    through exceed twice the 256 MB Infinity Cache (at least 2, at most 8)."""
+    return max(2, min(8, int(2 * 256e6 // nbytes) + 1))
+
+
+def _check(pkg, rc, what):
+    if rc != 0:
+        raise pkg.GpuError(rc, what)
+
+
+def layer_lines(pkg, torch, stream, lib, shapes, sigma, n_toks, seed):
+    """One line per token count: each matrix of the layer (Q4_K; lm_head
+    Q8_0) timed alone over rotated weight copies -- swamp_qgemv at 1 token,
+    swamp_qgemv_batched above (the reference's fused_gemv_q4k /
+    fused_gemv_q4k_batched calls of benchmark_q4k_batched.rs:70-108, y
+    overwritten, which equals its zero-fill plus accumulate) -- then summed:
+    GB/s over the algorithmic bytes (W + N K 4 + N rows 4) and GFLOP/s over
+    2 N rows K (benchmark_q4k_batched.rs:92-94)."""
+    s = stream.cuda_stream
+    bpw = {pkg.Q4_K: 144 / 256, pkg.Q8_0: 34 / 32}
+    mats = []
+    for i, (name, rows, k) in enumerate(shapes):
+        dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
+        d0 = torch.from_numpy(pkg.synth_quantized(dt, seed ^ 0x300 ^ i, sigma, rows, k)).cuda()
+        n_cp = _copies(rows * k * bpw[dt])
+        mats.append((name, dt, rows, k, [d0] + [d0.clone() for _ in range(n_cp - 1)]))
+    out = []
+    for n_tok in n_toks:
+        per, tot_b, tot_us = [], 0, 0.0
+        for i, (name, dt, rows, k, ws) in enumerate(mats):
+            x = torch.from_numpy(pkg.fill_normal(seed ^ 0x400 ^ i, 1.0, n_tok, k)).cuda()
+            y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+            n_cp = len(ws)
+            if n_tok == 1:
+                fn = lambda c: _check(pkg, lib.swamp_qgemv(dt, ws[c % n_cp].data_ptr(),
+                                                           ws[0].numel(), x.data_ptr(),
+                                                           y.data_ptr(), rows, k, s),
+                                      "swamp_qgemv")
+            else:
+                fn = lambda c: _check(pkg, lib.swamp_qgemv_batched(
+                    dt, ws[c % n_cp].data_ptr(), ws[0].numel(), x.data_ptr(), y.data_ptr(),
+                    n_tok, rows, k, 0, s), "swamp_qgemv_batched")
+            us = _timed(torch, stream, fn)
+            b = int(rows * k * bpw[dt]) + n_tok * k * 4 + n_tok * rows * 4
+            per.append({"name": name, "dtype": pkg.DTYPE_NAMES[dt], "rows": rows, "k": k,
+                        "us": round(us, 2), "GB/s": round(b / us / 1e3, 1)})
+            tot_b += b
+            tot_us += us
+            del x, y
+        flop = sum(2 * n_tok * r * k for _, _, r, k, _ in mats)
+        out.append({"n_tok": n_tok, "alg_bytes": tot_b, "us": round(tot_us, 1),
+                    "GB/s": round(tot_b / tot_us / 1e3, 1),
+                    "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                    "GFLOP/s": round(flop / tot_us / 1e3, 1), "matrices": per})
+    del mats
+    return out
+
+
+def prefill_70b_lines(pkg, torch, np, stream, lib, names, m=4096):
+    """The 4096-token bf16 prefill GEMM at 70B shapes (Q4_K weights): mean of
+    5 calls after 3 untimed ones per matrix; TFLOP/s over 2 M rows K."""
+    s = stream.cuda_stream
+    per = []
+    for i, (name, rows, k) in enumerate(SWEEP_70B):
+        if name not in names:
+            continue
+        dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
+        w = torch.from_numpy(pkg.synth_quantized(dt, SEED ^ 0x500 ^ i, 0.015, rows, k)).cuda()
+        xb = torch.from_numpy(pkg.to_bf16_bits(
+            pkg.fill_normal(SEED ^ 0x600 ^ i, 1.0, m, k)).view(np.int16)).cuda()
+        y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+        fn = lambda c: _check(pkg, lib.swamp_qgemm(dt, w.data_ptr(), w.numel(), xb.data_ptr(),
+                                                   pkg.BF16, y.data_ptr(), m, rows, k, s),
+                              "swamp_qgemm")
+        us = _timed(torch, stream, fn, reps=5)
+        tf = 2 * m * rows * k / us / 1e6
+        per.append({"name": name, "m": m, "dtype": pkg.DTYPE_NAMES[dt], "rows": rows, "k": k,
+                    "x": "bf16", "us": round(us, 1), "TFLOP/s": round(tf, 1),
+                    "frac_peak": round(tf / BF16_PEAK_TFLOPS, 4), "peak": BF16_PEAK_TFLOPS})
+        del w, xb, y
+    return per
+
+
 def run_sweep(pkg, torch, np, stream, lib):
     """Extra lines (opt-in, --sweep): the small-batch Q4_K sweep at 8B shapes
-    (lm_head Q8_0) for 1, 2, 4, 8, 16, 17, 24, 32 and 64 tokens (17-64 in token
-    groups of 16), the 70B Q4_K layer as
-    batch-1 decode, the 8B shapes in Q6_K at 1, 2, 4, 16 and 32 tokens, the 70B
-    layer as a 4096-token bf16 prefill GEMM, and the 8B layer (without
-    lm_head) as a 2048-token int8 GEMM with Q4_K and Q4_0 weights.  Each matrix is
-    timed alone: 20 launches over 3 rotated weight copies behind a GPU
-    sleep; GB/s over the algorithmic bytes, TFLOP/s over 2*M*rows*K."""
+    (lm_head Q8_0) for 2, 17, 24, 32 and 64 tokens (17-64 in token groups of
+    16), the 8B shapes in Q6_K at 1, 2, 4, 16 and 32 tokens, the activation
+    producers, the 70B O-projection and lm_head as 4096-token bf16 prefill
+    GEMMs, and the 8B layer (without lm_head) as a 2048-token int8 GEMM with
+    Q4_K and Q4_0 weights.  Each matrix is timed alone: 20 launches over
+    rotated weight copies behind a GPU sleep; GB/s over the algorithmic
+    bytes, TFLOP/s over 2*M*rows*K."""
     s = stream.cuda_stream
     bpw = {pkg.Q4_0: 18 / 32, pkg.Q4_K: 144 / 256, pkg.Q8_0: 34 / 32, pkg.Q6_K: 210 / 256}
 
@@ -310,37 +435,10 @@ def run_sweep(pkg, torch, np, stream, lib):
         if rc != 0:
             raise pkg.GpuError(rc, what)
 
-    for label, shapes, sigma in (("llama3-8b", SWEEP_8B, 0.02), ("llama3-70b", SWEEP_70B, 0.015)):
-        for n_tok in ((1, 2, 4, 8, 16, 17, 24, 32, 64) if label == "llama3-8b" else (1,)):
-            per, tot_b, tot_us = [], 0, 0.0
-            for i, (name, rows, k) in enumerate(shapes):
-                dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
-                copies = max(2, min(8, int(2 * 256e6 // (rows * k * bpw[dt])) + 1))
-                ws = weights_dev(dt, rows, k, SEED ^ 0x300 ^ i, sigma, copies)
-                x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x400 ^ i, 1.0, n_tok, k)).cuda()
-                y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
-                if n_tok == 1:
-                    fn = lambda c: check(lib.swamp_qgemv(dt, ws[c % copies].data_ptr(), ws[0].numel(),
-                                                         x.data_ptr(), y.data_ptr(), rows, k, s),
-                                         "swamp_qgemv")
-                else:
-                    fn = lambda c: check(lib.swamp_qgemv_batched(
-                        dt, ws[c % copies].data_ptr(), ws[0].numel(), x.data_ptr(), y.data_ptr(),
-                        n_tok, rows, k, 0, s), "swamp_qgemv_batched")
-                us = timed(fn)
-                b = int(rows * k * bpw[dt]) + n_tok * k * 4 + n_tok * rows * 4
-                per.append({"name": name, "dtype": "Q8_0" if dt == pkg.Q8_0 else "Q4_K",
-                            "rows": rows, "k": k, "us": round(us, 2),
-                            "GB/s": round(b / us / 1e3, 1),
-                            "TFLOP/s": round(2 * n_tok * rows * k / us / 1e6, 2)})
-                tot_b += b
-                tot_us += us
-                del ws, x, y
-            print(json.dumps({"sweep": f"{label} decode/small-batch Q4_K (lm_head Q8_0)",
-                              "n_tok": n_tok, "alg_bytes": tot_b, "us": round(tot_us, 1),
-                              "GB/s": round(tot_b / tot_us / 1e3, 1),
-                              "frac_hbm_peak": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
-                              "matrices": per}), flush=True)
+    # token counts beyond the main line's: 2 (two-token GEMV), 17-64 (token groups)
+    for line in layer_lines(pkg, torch, stream, lib, SWEEP_8B, 0.02, (2, 17, 24, 32, 64), SEED):
+        print(json.dumps({"sweep": "llama3-8b small-batch Q4_K (lm_head Q8_0)", **line}),
+              flush=True)
     # every 8B matrix in Q6_K (Q4_K_M files keep lm_head and part of attn_v /
     # ffn_down in Q6_K): batch-1 decode, and small batches of 2, 4, 16 and 32
     # tokens (one pass each)
@@ -402,27 +500,11 @@ def run_sweep(pkg, torch, np, stream, lib):
         del a0, o
     print(json.dumps({"sweep": "llama3-8b prefill activation producers -> bf16, 2048 tokens",
                       "kernels": per}), flush=True)
-    # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights (lm_head Q8_0)
-    m = 4096
-    per = []
-    for i, (name, rows, k) in enumerate(SWEEP_70B):
-        dt = pkg.Q8_0 if name == "lm_head" else pkg.Q4_K
-        ws = weights_dev(dt, rows, k, SEED ^ 0x500 ^ i, 0.015, 1)
-        xb = torch.from_numpy(pkg.to_bf16_bits(
-            pkg.fill_normal(SEED ^ 0x600 ^ i, 1.0, m, k)).view(np.int16)).cuda()
-        y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
-        fn = lambda c: check(lib.swamp_qgemm(dt, ws[0].data_ptr(), ws[0].numel(),
-                                             xb.data_ptr(), pkg.BF16, y.data_ptr(), m, rows, k,
-                                             s), "swamp_qgemm")
-        us = timed(fn, reps=5)
-        tf = 2 * m * rows * k / us / 1e6
-        per.append({"name": name, "dtype": "Q8_0" if dt == pkg.Q8_0 else "Q4_K",
-                    "rows": rows, "k": k, "us": round(us, 1),
-                    "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
-        del ws, xb, y
+    # 70B prefill, 4096 tokens, bf16 activations, Q4_K weights (lm_head Q8_0):
+    # the matrices the main line leaves out
     print(json.dumps({"sweep": "llama3-70b prefill Q4_K (lm_head Q8_0) x bf16, 4096 tokens",
-                      "matrices": per}),
-          flush=True)
+                      "matrices": prefill_70b_lines(pkg, torch, np, stream, lib,
+                                                    ("o_proj", "lm_head"))}), flush=True)
     # 8B prefill, 2048 tokens, Q4_K weights on the int8 MFMA against Q8_0 x
     # (quantizer included), beside the same calls with Q4_0 weights
     m = 2048
@@ -556,13 +638,18 @@ def main():
     ap.add_argument("--settle", type=float, default=0.3,
                     help="seconds of untimed decode steps before the warm-up steps")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-small-batch", action="store_true",
+                    help="leave out the 8B Q4_K small-batch lines and their CPU lines")
+    ap.add_argument("--no-70b", action="store_true",
+                    help="leave out the 70B decode layer and 4096-token prefill lines")
     ap.add_argument("--cpu-threads", type=str, default="6,max",
                     help="thread counts of the CPU baseline, comma-separated; 'max' is every "
                          "thread of this host's share (the reference's pool size is 6)")
     ap.add_argument("--copies", type=int, default=3, help="weight-set copies rotated per step")
     ap.add_argument("--sweep", action="store_true",
-                    help="also print one line per extra workload (8B small-batch Q4_K sweep, "
-                         "70B decode and prefill) after the main line")
+                    help="also print one line per extra workload (more token counts, Q6_K, "
+                         "producers, the rest of the 70B prefill, int8 with Q4_K) after the "
+                         "main line")
     ap.add_argument("--pmc-batched", type=int, default=0, metavar="N",
                     help="only run 5 swamp_qgemv_batched launches of N tokens on each 8B sweep "
                          "matrix (Q4_K, lm_head Q8_0), for rocprofv3 --pmc counter passes; no JSON")
@@ -873,12 +960,32 @@ def main():
                                     "peak": peak})
                 del w, x, y, xf_d, xq
 
+    # ---- 8B Q4_K small batch (lm_head Q8_0) at 1, 4, 8, 16 tokens; 70B Q4_K
+    # decode layer (lm_head Q8_0) and 4096-token bf16 prefill --------------------
+    small = None
+    if not args.no_small_batch:
+        small = {"workload": "llama3-8b Q4_K qkv 6144x4096, o_proj 4096x4096, gate_up "
+                             "28672x4096, down 4096x14336 + lm_head 128256x4096 Q8_0; "
+                             "W ~ N(0,0.02), x ~ N(0,1) fp32; each matrix timed alone "
+                             "(mean of 20 launches over rotated weight copies), summed",
+                 "lines": layer_lines(pkg, torch, stream, lib, SWEEP_8B, 0.02, (1, 4, 8, 16),
+                                      SEED)}
+    dec70 = pre70 = None
+    if not args.no_70b:
+        dec70 = {"workload": "llama3-70b Q4_K qkv 10240x8192, o_proj 8192x8192, gate_up "
+                             "57344x8192, down 8192x28672 + lm_head 128256x8192 Q8_0, batch 1; "
+                             "W ~ N(0,0.015), x ~ N(0,1) fp32; each matrix timed alone, summed",
+                 **layer_lines(pkg, torch, stream, lib, SWEEP_70B, 0.015, (1,), SEED ^ 0x70B)[0]}
+        pre70 = prefill_70b_lines(pkg, torch, np, stream, lib, ("gate_up", "down", "qkv"))
+
     tcounts = []
     for t in args.cpu_threads.split(","):
         n_t = cpu_threads_available() if t.strip() == "max" else int(t)
         if n_t not in tcounts:
             tcounts.append(n_t)
     cpu = None if args.no_cpu else cpu_baseline(pkg, tcounts)
+    if small is not None and not args.no_cpu:
+        small["cpu"] = cpu_small_batch(pkg, tcounts)
 
     out = {
         "metric": "decode Q4 GEMV HBM GB/s (% peak) at 8B shapes; prefill GEMM TOPS @2048 tok",
@@ -903,6 +1010,9 @@ def main():
         "shapes": shapes,
         "decode_f16x": f16x,
         "prefill": prefill,
+        "small_batch": small,
+        "decode_70b": dec70,
+        "prefill_70b": pre70,
     }
     print(json.dumps(out), flush=True)
     if args.sweep:

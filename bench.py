@@ -603,7 +603,8 @@ def route_times(pkg, torch, s):
 
 def route_crossover():
     """The prefill GEMM's two routes side by side: each timed in a child
-    process with SWAMP_GEMM_ROUTE set (the library reads it once)."""
+    process with SWAMP_GEMM_ROUTE set (so that neither route's first calls
+    share a process with the other's)."""
     import subprocess
     res = {}
     for route in ("fused", "dq"):

@@ -569,6 +569,35 @@ def stream_reference(torch):
     return out
 
 
+def mfma_probe(iters=8000, reps=3):
+    """The matrix-core issue microbenchmark (csrc/probe_mfma.hip): one
+    workgroup per CU issuing bf16 32x32x16 MFMAs with V VALU fmas per MFMA
+    in the same wave (kind 0, one wave per SIMD), in both of two waves per
+    SIMD (kind 1) or in a second wave beside an MFMA-only one (kind 2), with
+    constant or random operands and with or without a 16-byte LDS fragment
+    read per MFMA."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(REPO, "llamanyon.rs_amd", "libswamp_probe.so"))
+    kinds = {0: "1 wave/SIMD, VALU in the MFMA wave", 1: "2 waves/SIMD, both MFMA + VALU",
+             2: "2 waves/SIMD, MFMA wave + VALU wave"}
+    n = lib.swamp_probe_mfma_configs(-1, None, None, None, None)
+    rows = []
+    for i in range(n):
+        kind, valu, rnd, lds = (ctypes.c_int() for _ in range(4))
+        lib.swamp_probe_mfma_configs(i, ctypes.byref(kind), ctypes.byref(valu), ctypes.byref(rnd),
+                                     ctypes.byref(lds))
+        ms, mfmas = ctypes.c_float(), ctypes.c_double()
+        if lib.swamp_probe_mfma_run(i, iters, reps, ctypes.byref(ms), ctypes.byref(mfmas)) != 0:
+            raise RuntimeError(f"swamp_probe_mfma_run({i}) failed")
+        tf = mfmas.value * 32768.0 / (ms.value * 1e-3) / 1e12
+        rows.append({"kind": kinds[kind.value], "valu_per_mfma": valu.value,
+                     "operands": "random" if rnd.value else "constant",
+                     "lds_read_per_mfma": bool(lds.value), "ms": round(ms.value, 3),
+                     "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
+    return {"mfma_probe": "V_MFMA_F32_32X32X16_BF16 throughput, one workgroup per CU",
+            "configs": rows}
+
+
 def route_times(pkg, torch, s):
     """us per swamp_qgemm call (Q4_0 weights, bf16 x; mean of 20 after 10
     warm-up calls) for each 8B shape and prompt length, through whichever
@@ -666,6 +695,10 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only run the matrix-core issue microbenchmark (libswamp_probe.so): "
+                         "bf16 MFMA throughput with VALU work in the same or a second wave per "
+                         "SIMD, random or constant operands, LDS fragment reads; one JSON line")
     ap.add_argument("--stream-ref", action="store_true",
                     help="only time torch's own streaming kernels over 1 GiB of fp32 (sum and "
                          "amax: one read; copy: one read and one write) as a reference for the "
@@ -695,6 +728,9 @@ def main():
 
     if args.route_times:
         print(json.dumps(route_times(pkg, torch, s)), flush=True)
+        return
+    if args.mfma_probe:
+        print(json.dumps(mfma_probe()), flush=True)
         return
     if args.stream_ref:
         print(json.dumps(stream_reference(torch)), flush=True)

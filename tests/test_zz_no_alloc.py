@@ -3,8 +3,12 @@ variant of swamp_qgemv_batched, with its scratch in a fixed per-GPU device
 array.  Through the C ABI, each call's output is compared bit for bit with
 swamp_qgemv_batched on the same inputs (both sum split reductions in a fixed
 order), on two calls in a row, the second with a smaller input, and with
-the oracle; a call whose scratch exceeds the array is refused before
-anything is launched."""
+the oracle; on a fresh stream the calls leave the device's default memory
+pool (where the library's per-stream scratch comes from) untouched, while
+the same calls through swamp_qgemv_batched take from it; a call whose
+scratch exceeds the array is refused before anything is launched."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -61,6 +65,47 @@ def test_noalloc_matches_batched_two_calls(pkg, orc, torch_dev, errlog):
         err = errlog(f"noalloc {dtype} n_tok={n_tok} {rows}x{cols} acc={acc}",
                      orc.normalized_error(outs[0], ref, deq, xs), path="noalloc")
         assert err <= 1e-3
+
+
+HIP_MEMPOOL_USED_MEM_CURRENT = 7  # hipMemPoolAttrUsedMemCurrent
+
+
+def _pool_used(torch):
+    """Bytes in use from the current device's default memory pool (the pool
+    hipMallocAsync draws from), through the HIP runtime torch has loaded."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    dev = torch.cuda.current_device()
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), dev) == 0
+    used = ctypes.c_uint64()
+    assert hip.hipMemPoolGetAttribute(pool, HIP_MEMPOOL_USED_MEM_CURRENT, ctypes.byref(used)) == 0
+    return used.value
+
+
+def test_noalloc_allocates_nothing(pkg, torch_dev):
+    """On a stream the library has never seen, swamp_qgemv_batched would
+    allocate its scratch from the default pool (the positive control below);
+    swamp_qgemv_batched_noalloc with the same scratch-taking shape must not."""
+    torch = torch_dev
+    L = pkg.gpu_lib()
+    dtype, n_tok, rows, cols = Q4_K, 16, 4096, 14336  # K groups: partial sums in scratch
+    assert L.swamp_qgemv_batched_workspace(dtype, n_tok, rows, cols, 0) > 0
+    raw, xs, d_w, d_x = _case(pkg, torch, dtype, n_tok, rows, cols, 5)
+    d_y = torch.empty((n_tok, rows), dtype=torch.float32, device="cuda")
+    print("[gpu case] noalloc leaves the default memory pool untouched", flush=True)
+    for fn, allocates in ((L.swamp_qgemv_batched_noalloc, False), (L.swamp_qgemv_batched, True)):
+        cs = torch.cuda.Stream()  # a stream without a library buffer
+        torch.cuda.synchronize()
+        before = _pool_used(torch)
+        for _ in range(2):
+            assert fn(dtype, d_w.data_ptr(), raw.size, d_x.data_ptr(), d_y.data_ptr(), n_tok, rows,
+                      cols, 0, cs.cuda_stream) == 0
+        torch.cuda.synchronize()
+        after = _pool_used(torch)
+        if allocates:
+            assert after > before, (before, after)
+        else:
+            assert after == before, (before, after)
 
 
 def test_noalloc_rejects_oversized_scratch(pkg, torch_dev):

@@ -45,6 +45,7 @@ Also reported (outside the timed steps):
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--no-small-batch] [--no-70b] [--cpu-threads 6,max]
                        [--sweep] [--pmc-probe] [--pmc-gemm] [--pmc-batched N]
+                       [--gemv-stages] [--gemv-fixed-cost] [--mfma-probe]
 --sweep adds one JSON line per extra workload after the main line: the
 Q4_K small batch at 2, 17, 24, 32 and 64 tokens (2 as one GEMV, 17-64 in
 token groups of 16) at 8B shapes, the 8B shapes in Q6_K, the activation
@@ -53,6 +54,10 @@ weights.  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
 --pmc-gemm the same for the 2048-token gate+up prefill GEMM; --pmc-batched N
 runs 5 small-batch launches of N tokens per 8B sweep matrix, for counter passes.
+--gemv-stages times the stages inside each 8B decode GEMV launch (stage
+stamps of libswamp_gpu_stamps.so), --gemv-fixed-cost the decode GEMV against
+row count, --mfma-probe the matrix-core issue microbenchmark; each prints
+one JSON line and nothing else.
 """
 from __future__ import annotations
 
@@ -569,6 +574,123 @@ def stream_reference(torch):
     return out
 
 
+def gemv_fixed_cost(pkg, torch, stream, lib):
+    """Decode GEMV time against row count at fixed K (Q4_0, fp32 x; mean of
+    50 launches over rotated weight copies behind a GPU sleep): the
+    intercept is the fixed cost of a launch, the slope the streaming rate.
+    Beside it, a one-element torch fill timed the same way: the period of
+    back-to-back launches of a kernel that does nothing."""
+    s = stream.cuda_stream
+
+    def timed(fn, reps=50):
+        for i in range(5):
+            fn(i)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(20_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    out = {"gemv_fixed_cost": "swamp_qgemv Q4_0 fp32 x, us and GB/s against rows", "lines": []}
+    for k in (4096, 14336):
+        pts = []
+        for rows in (64, 512, 1024, 2048, 4096, 6144, 8192, 16384, 28672):
+            raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0xF00 ^ rows, 0.02, rows, k)
+            n_cp = max(2, min(16, int(600e6 // raw.size) + 1))
+            d0 = torch.from_numpy(raw).cuda()
+            ws = [d0] + [d0.clone() for _ in range(n_cp - 1)]
+            x = torch.from_numpy(pkg.fill_normal(SEED ^ 0xF01, 1.0, 1, k)[0]).cuda()
+            y = torch.empty(rows, dtype=torch.float32, device="cuda")
+            us = timed(lambda c: _check(pkg, lib.swamp_qgemv(pkg.Q4_0, ws[c % n_cp].data_ptr(),
+                                                             raw.size, x.data_ptr(), y.data_ptr(),
+                                                             rows, k, s), "swamp_qgemv"))
+            pts.append({"rows": rows, "bytes": int(raw.size), "us": round(us, 2),
+                        "GB/s": round(raw.size / us / 1e3, 1)})
+            del ws, d0, x, y
+        a, b = pts[-2], pts[-1]
+        out["lines"].append({"k": k, "points": pts,
+                             "slope_GB/s": round((b["bytes"] - a["bytes"]) / (b["us"] - a["us"]) / 1e3, 1)})
+    one = torch.empty(1, dtype=torch.float32, device="cuda")
+    out["empty_kernel_period_us"] = round(timed(lambda c: one.fill_(1.0)), 2)
+    return out
+
+
+def gemv_stages(pkg, torch, stream, reps=5):
+    """Where a decode GEMV launch spends its time: libswamp_gpu_stamps.so
+    (libswamp_gpu.so with the decode GEMV's stage stamps compiled in) runs
+    each 8B Q4_0 matrix (fp32 x) after 20 warm launches over rotated weight
+    copies; every wave records the real-time counter at kernel entry, x
+    landed, x fragment built, first tile stored and last tile stored.
+    Times are microseconds from the first wave's entry, median over waves
+    (and over `reps` launches), with the last wave's end; beside them the
+    launch's duration from HIP events (which adds the dispatch before the
+    first wave starts and the completion after the last ends)."""
+    import ctypes
+    import numpy as np
+    lib = ctypes.CDLL(os.path.join(REPO, "llamanyon.rs_amd", "libswamp_gpu_stamps.so"))
+    lib.swamp_gemv_stage_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    lib.swamp_qgemv.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    if lib.swamp_gpu_init() != 0:
+        raise RuntimeError("swamp_gpu_init failed (stamps library)")
+    s = stream.cuda_stream
+    n_slots = 16384 * 8
+    buf = np.zeros(n_slots, dtype=np.uint64)
+    names = ["entry", "x_landed", "xfrag_built", "first_tile_stored", "last_tile_stored"]
+    out = {"gemv_stages": "swamp_qgemv Q4_0 fp32 x, us from the first wave's entry", "shapes": []}
+    for i, (name, rows, k) in enumerate(DECODE_SHAPES):
+        raw = pkg.synth_quantized(pkg.Q4_0, SEED ^ 0x700 ^ i, 0.02, rows, k)
+        n_cp = max(2, min(8, int(900e6 // raw.size) + 1))
+        d0 = torch.from_numpy(raw).cuda()
+        ws = [d0] + [d0.clone() for _ in range(n_cp - 1)]
+        x = torch.from_numpy(pkg.fill_normal(SEED ^ 0x701, 1.0, 1, k)[0]).cuda()
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+
+        def launch(c):
+            rc = lib.swamp_qgemv(pkg.Q4_0, ws[c % n_cp].data_ptr(), raw.size, x.data_ptr(),
+                                 y.data_ptr(), rows, k, s)
+            if rc != 0:
+                raise pkg.GpuError(rc, "swamp_qgemv (stamps library)")
+        per = {n: [] for n in names[1:]}
+        ends, spreads, durs, waves = [], [], [], 0
+        for r in range(reps):
+            for c in range(20):
+                launch(c)
+            torch.cuda.synchronize()
+            if lib.swamp_gemv_stage_stamps(buf.ctypes.data, 0, 1) != 0:
+                raise RuntimeError("swamp_gemv_stage_stamps failed")
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            launch(21 + r)  # keeps the card busy up to the timed launch
+            e0.record(stream)
+            launch(22 + r)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            durs.append(e0.elapsed_time(e1) * 1e3)
+            if lib.swamp_gemv_stage_stamps(buf.ctypes.data, n_slots, 1) != 0:
+                raise RuntimeError("swamp_gemv_stage_stamps failed")
+            t = buf.reshape(-1, 8)[:, :5].astype(np.int64)
+            t = t[(t[:, 0] > 0) & (t[:, 4] > 0)]
+            waves = len(t)
+            rel = (t - t[:, 0].min()) * 0.01  # 100 MHz counter -> us
+            for j, n in enumerate(names[1:], start=1):
+                per[n].append(float(np.median(rel[:, j])))
+            ends.append(float(rel[:, 4].max()))
+            spreads.append(float(rel[:, 0].max()))
+        line = {"name": name, "rows": rows, "k": k, "waves": waves,
+                "event_us": round(float(np.median(durs)), 2),
+                "entry_spread_us": round(float(np.median(spreads)), 2)}
+        for n in names[1:]:
+            line[n + "_us"] = round(float(np.median(per[n])), 2)
+        line["last_wave_end_us"] = round(float(np.median(ends)), 2)
+        out["shapes"].append(line)
+        del ws, d0, x, y
+    return out
+
+
 def mfma_probe(iters=8000, reps=3):
     """The matrix-core issue microbenchmark (csrc/probe_mfma.hip): one
     workgroup per CU issuing bf16 32x32x16 MFMAs with V VALU fmas per MFMA
@@ -695,6 +817,12 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
+    ap.add_argument("--gemv-fixed-cost", action="store_true",
+                    help="only time the decode GEMV (Q4_0) against row count at K = 4096 and "
+                         "14336, beside an empty kernel's launch period; one JSON line")
+    ap.add_argument("--gemv-stages", action="store_true",
+                    help="only time the stages of each 8B decode GEMV launch (stage stamps of "
+                         "libswamp_gpu_stamps.so: x landed, first tile, last tile); one JSON line")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only run the matrix-core issue microbenchmark (libswamp_probe.so): "
                          "bf16 MFMA throughput with VALU work in the same or a second wave per "
@@ -731,6 +859,12 @@ def main():
         return
     if args.mfma_probe:
         print(json.dumps(mfma_probe()), flush=True)
+        return
+    if args.gemv_stages:
+        print(json.dumps(gemv_stages(pkg, torch, stream)), flush=True)
+        return
+    if args.gemv_fixed_cost:
+        print(json.dumps(gemv_fixed_cost(pkg, torch, stream, pkg.gpu_lib())), flush=True)
         return
     if args.stream_ref:
         print(json.dumps(stream_reference(torch)), flush=True)

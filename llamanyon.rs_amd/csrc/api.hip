@@ -131,7 +131,6 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
   };
   static std::mutex mu;
   static std::vector<Entry> cache;
-  static std::vector<void *> retired;  // replaced buffers a graph may hold (never freed)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   const std::thread::id tid =
@@ -155,11 +154,10 @@ void *stream_workspace(hipStream_t s, size_t bytes) {
     return nullptr;
   }
   if (e) {
-    // A buffer a captured call used stays allocated until the process ends
-    // (the graph's replays write it); any other is released after the work
-    // already queued on s.
-    if (e->captured) retired.push_back(e->p);
-    else (void)hipFreeAsync(e->p, s);
+    // A buffer a captured call used is never released: the graph's replays
+    // write it until the process ends.  Any other is released after the
+    // work already queued on s.
+    if (!e->captured) (void)hipFreeAsync(e->p, s);
     e->p = p;
     e->bytes = bytes;
     e->captured = false;

@@ -214,3 +214,22 @@ int swamp_launch_gemv_multi(int n_mats, const uint32_t *dtypes, const void *cons
   return launch_multi<kProNone, true>(n_mats, dtypes, d_ws, row_counts, d_x, Pro{}, d_ys, n_cols,
                                       s);
 }
+
+#ifdef SWAMP_STAGE_STAMPS
+// Measurement build only: copy the first n stamp slots (8 per wave, five
+// used) to host memory, then clear them when reset is set.  0 on success.
+extern "C" __attribute__((visibility("default"))) int swamp_gemv_stage_stamps(uint64_t *host,
+                                                                               int n, int reset) {
+  if (n < 0 || n > kStampWaves * 8) return SWAMP_EINVAL;
+  if (n && hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gemv_stamps), size_t(n) * 8, 0,
+                               hipMemcpyDeviceToHost) != hipSuccess)
+    return SWAMP_ELAUNCH;
+  if (reset) {
+    static uint64_t zeros[kStampWaves * 8];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_gemv_stamps), zeros, sizeof(zeros), 0,
+                          hipMemcpyHostToDevice) != hipSuccess)
+      return SWAMP_ELAUNCH;
+  }
+  return SWAMP_OK;
+}
+#endif

@@ -523,6 +523,30 @@ __device__ __forceinline__ float item_dot(const Raw<DT> &r, const XFrag32<DT> &x
   }
 }
 
+// ---- stage stamps (measurement build) ------------------------------------
+// Built with SWAMP_STAGE_STAMPS (libswamp_gpu_stamps.so, bench.py
+// --gemv-stages), each wave of the decode GEMV records the real-time
+// counter (100 MHz) at five points: kernel entry, x landed in LDS (after
+// the staging barrier), x fragment built, first tile stored, last tile
+// stored.  The regular build compiles the marks away.
+#ifdef SWAMP_STAGE_STAMPS
+constexpr int kStampWaves = 16384;
+__device__ uint64_t g_gemv_stamps[kStampWaves * 8];
+struct Stamps {
+  uint64_t t[5] = {};
+  __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+  __device__ __forceinline__ void put(int wave_id, int lane) {
+    if (lane == 0 && wave_id < kStampWaves)
+      for (int i = 0; i < 5; i++) g_gemv_stamps[size_t(wave_id) * 8 + i] = t[i];
+  }
+};
+#else
+struct Stamps {
+  __device__ __forceinline__ void mark(int) {}
+  __device__ __forceinline__ void put(int, int) {}
+};
+#endif
+
 // ---- wavefront reduction of kRows partial sums ---------------------------
 
 template <int kCtrl>
@@ -749,6 +773,8 @@ __global__ void __launch_bounds__(64 * kWaves * kSets)
   __shared__ float red[2][kSets][kWaves][kRows];
   const int tid = kSets == 1 ? int(threadIdx.x) : int(threadIdx.x) % T;
   const int set = kSets == 1 ? 0 : __builtin_amdgcn_readfirstlane(int(threadIdx.x) / T);
+  Stamps st;
+  st.mark(0);
 
   int item[kPPT];
   bool valid[kPPT];
@@ -814,6 +840,7 @@ __global__ void __launch_bounds__(64 * kWaves * kSets)
     // (the accumulating form's first y load is issued before the staging).
     constexpr int kAfter = kRows * loads_per_item(DT);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kAfter) : "memory");
+    st.mark(1);
     read_vec(x4[0], xlds, item[0]);
     if constexpr (kTwo) {
       read_vec(v4[0], xlds + kRegion, item[0]);
@@ -880,7 +907,9 @@ __global__ void __launch_bounds__(64 * kWaves * kSets)
   // past the end; with kUniform every set stops when set 0's is, a set
   // whose tile is past the end working through a stand-in (its current
   // tile, clamped) that it does not store.
+  st.mark(2);
   int base = int(blockIdx.x) * kSets;
+  bool first_trip = true;
   for (;;) {
     const int cur = tile;  // the tile ra holds (clamped)
     int nb = base + stride;
@@ -891,6 +920,8 @@ __global__ void __launch_bounds__(64 * kWaves * kSets)
     __builtin_amdgcn_sched_barrier(0);
     consume_tile<DT, kPPT, kRows, kWaves, kAcc>(ra, xf, ta, item, red[0][set], tid, m, out_scale,
                                                 ya, live_a);
+    if (first_trip) st.mark(3);
+    first_trip = false;
     if (kUniform ? nb >= n_tiles : !live_b) break;
     base = __builtin_amdgcn_readfirstlane(nb);  // keep it scalar (no VGPR round trip)
     tile = live_b ? base + set : cur;           // the tile rb holds
@@ -906,6 +937,8 @@ __global__ void __launch_bounds__(64 * kWaves * kSets)
     base = __builtin_amdgcn_readfirstlane(nb);  // keep it scalar (no VGPR round trip)
     tile = live_a ? base + set : tile;          // the tile ra holds
   }
+  st.mark(4);
+  st.put(int(blockIdx.x) * kWaves * kSets + int(threadIdx.x >> 6), int(threadIdx.x & 63));
 }
 
 

@@ -61,6 +61,19 @@ def test_gpu_lib_exports_nothing_else(pkg):
     assert not extra, extra
 
 
+def test_stamps_library_is_the_product_plus_one_export(pkg):
+    """libswamp_gpu_stamps.so (bench.py --gemv-stages) exports what the
+    product does plus swamp_gemv_stage_stamps; the product does not export
+    it (its stamps are compiled away)."""
+    path = os.path.join(os.path.dirname(pkg.GPU_LIB_PATH), "libswamp_gpu_stamps.so")
+    if not os.path.exists(path):
+        pytest.skip("libswamp_gpu_stamps.so not built")
+    prod = {n for n in exported(pkg.GPU_LIB_PATH) if not n.startswith("__hip_cuid_")}
+    stamps = {n for n in exported(path) if not n.startswith("__hip_cuid_")}
+    assert stamps - prod == {"swamp_gemv_stage_stamps"}
+    assert prod <= stamps
+
+
 def test_quant_lib_exports_header(pkg):
     names = declared("swamp_quant.h")
     assert set(names) == set(pkg.QUANT_SYMBOLS)

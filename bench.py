@@ -381,6 +381,22 @@ def layer_lines(pkg, torch, stream, lib, shapes, sigma, n_toks, seed):
     return out
 
 
+def gemm_route(torch, dtype_q6k, m, rows, k, x_name):
+    """Which of the library's kernels a swamp_qgemm call runs, by the rule
+    of swamp_gemm_dq_route (csrc/gemm_dq.hip): bf16 x takes the
+    dequantize-once route (blocks_to_bf16 + gemm_bb) for Q6_K, and from 1024
+    tokens for shapes whose 256 x 256 tiles fill more than half but not all
+    of the CUs; else the fused dequant GEMM (gemm_bf16_kernel).  Q8_0 x runs
+    the int8 GEMM."""
+    if x_name != "bf16":
+        return "gemm_i8 (int8 MFMA)"
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = ((m + 255) // 256) * ((rows + 255) // 256)
+    if dtype_q6k or (m >= 1024 and k >= 1024 and 2 * tiles > cus and tiles < cus):
+        return "dequantize-once: blocks_to_bf16 + gemm_bb (plain bf16 MFMA GEMM)"
+    return "fused dequant bf16 MFMA GEMM (gemm_bf16_kernel)"
+
+
 def prefill_70b_lines(pkg, torch, np, stream, lib, names, m=4096):
     """The 4096-token bf16 prefill GEMM at 70B shapes (Q4_K weights): mean of
     5 calls after 3 untimed ones per matrix; TFLOP/s over 2 M rows K."""
@@ -400,7 +416,8 @@ def prefill_70b_lines(pkg, torch, np, stream, lib, names, m=4096):
         us = _timed(torch, stream, fn, reps=5)
         tf = 2 * m * rows * k / us / 1e6
         per.append({"name": name, "m": m, "dtype": pkg.DTYPE_NAMES[dt], "rows": rows, "k": k,
-                    "x": "bf16", "us": round(us, 1), "TFLOP/s": round(tf, 1),
+                    "x": "bf16", "route": gemm_route(torch, dt == pkg.Q6_K, m, rows, k, "bf16"),
+                    "us": round(us, 1), "TFLOP/s": round(tf, 1),
                     "frac_peak": round(tf / BF16_PEAK_TFLOPS, 4), "peak": BF16_PEAK_TFLOPS})
         del w, xb, y
     return per
@@ -1128,6 +1145,7 @@ def main():
                     us = e0.elapsed_time(e1) * 1e3 / reps
                     tops = 2.0 * pm * rows * k / (us * 1e-6) / 1e12
                     prefill.append({"name": name, "m": pm, "rows": rows, "k": k, "x": xname,
+                                    "route": gemm_route(torch, False, pm, rows, k, xname),
                                     "us": round(us, 1), "TFLOP/s": round(tops, 1),
                                     "frac_peak": round(tops / peak, 4),
                                     "peak": peak})

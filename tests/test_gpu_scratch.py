@@ -72,6 +72,44 @@ def test_workspace_queries(pkg, torch_dev):
     assert L.swamp_workspace_reserve(None, 0) == 0
 
 
+def test_bench_route_labels_match_library(pkg, torch_dev, monkeypatch):
+    """bench.py names the kernels behind each prefill line by the library's
+    route rule.  The workspace the library asks for follows the route it
+    takes (SWAMP_GEMM_ROUTE forces one, read per call), so on every bench
+    shape whose two routes need different scratch, the default's scratch
+    names the route, and the label must agree with it."""
+    import importlib.util
+    import os
+    torch = torch_dev
+    spec = importlib.util.spec_from_file_location(
+        "bench_mod", os.path.join(os.path.dirname(os.path.dirname(__file__)), "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    L = pkg.gpu_lib()
+    shapes = [(Q4_0, m, rows, k) for m in (2048, 512) for _, rows, k in bench.PREFILL_SHAPES]
+    shapes += [(Q4_K, 4096, rows, k) for _, rows, k in bench.SWEEP_70B]
+    # either side of the 1024-token bound (224 tiles: more than half a round)
+    shapes += [(Q4_0, 1024, 14336, 4096), (Q4_0, 1000, 14336, 4096)]
+    checked = 0
+    for dt, m, rows, k in shapes:
+        def ws(route=None):
+            if route:
+                monkeypatch.setenv("SWAMP_GEMM_ROUTE", route)
+            else:
+                monkeypatch.delenv("SWAMP_GEMM_ROUTE", raising=False)
+            return L.swamp_qgemm_workspace(dt, BF16, m, rows, k)
+        ws_dq, ws_fused, ws_default = ws("dq"), ws("fused"), ws()
+        label = bench.gemm_route(torch, False, m, rows, k, "bf16")
+        if ws_dq == ws_fused:
+            continue
+        assert ws_default in (ws_dq, ws_fused), (dt, m, rows, k)
+        assert label.startswith("dequantize-once") == (ws_default == ws_dq), (dt, m, rows, k, label)
+        checked += 1
+    assert checked >= 6, checked
+    # Q6_K always takes the dequantize-once route
+    assert bench.gemm_route(torch, True, 64, 512, 4096, "bf16").startswith("dequantize-once")
+
+
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
 def test_gemm_int8_split_repeat_bitwise(pkg, orc, torch_dev, errlog, dtype):
     """The int8 GEMM's K pieces are summed in piece order: repeated calls,

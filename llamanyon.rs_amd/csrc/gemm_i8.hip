@@ -17,11 +17,16 @@
 //    int8 rows (Q4_0 nibbles become q - 8 with one byte-wise add and xor)
 //    plus per-block fp32 scales; two LDS stages, one barrier per step.
 //  * Each block's int32 32 x 32 result is converted and added into the
-//    fp32 accumulators with its two scales: three vector ops per output
-//    element per block (Q4_K four: the minimum term is one more FMA).  With a scale per 32-block on both sides this
-//    per-element work, not the matrix cores, bounds the kernel (the 32-deep
-//    int8 MFMA does 32 MACs per element in the time the vector ALU does
-//    about five element ops).
+//    fp32 accumulators with its scale product d_x d_w: two vector ops per
+//    output element per block (convert, FMA).  The products are an outer
+//    product of the block's scale vectors, d_x per token and d_w per weight
+//    row, and come from one V_MFMA_F32_32X32X1_2B_F32 per pair of tiles, in
+//    the int32 result's own layout.  They are exact: each is an fp16 times an
+//    fp16 (Q4_K: times d sc, an fp16 times a 6-bit code).  For Q4_K the same
+//    instruction adds the minimum term's outer product into the accumulators.
+//    With a scale per 32-block on both sides the per-element convert and FMA
+//    still bound the kernel: the 32-deep int8 MFMA does 32 MACs per element
+//    in the time the vector ALU does about five element ops.
 //  * The two MFMA operands are read with the same per-lane byte rule, so
 //    the dot over a block does not depend on how the instruction orders k
 //    inside the block.
@@ -39,7 +44,7 @@ using swamp::shr16;
 
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x32_t __attribute__((ext_vector_type(32)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 
@@ -207,55 +212,51 @@ __device__ __forceinline__ void lstore(uint8_t *stg, const Stage<DT> &st, const 
   }
 }
 
-// One K step (four blocks) on LDS stage `stg`.
+// One K step (four blocks) on LDS stage `stg`.  acc[j] holds the wave's two
+// 32 x 32 tiles of weight tile j: element 16 i + e is tile (i, j)'s element e.
 template <int DT>
-__device__ __forceinline__ void compute(f32x16_t (&acc)[2][2], const uint8_t *stg, int wm, int wn,
+__device__ __forceinline__ void compute(f32x32_t (&acc)[2], const uint8_t *stg, int wm, int wn,
                                         int lane) {
   const uint8_t *xq = stg, *wq = stg + kQBytes;
   const float *xs = reinterpret_cast<const float *>(stg + 2 * kQBytes);
   const float *wsc = xs + kBlk * kBM;
   const float *wmn = wsc + kBlk * kBM, *xsum = wmn + kBlk * kBM;  // Q4_K only
   const int fr = lane & 31, fc = lane >> 5;
-  // one block per trip, not unrolled: the sixteen int32 tiles of four
-  // unrolled blocks would all be live at once
+  // one block per trip, not unrolled: the int32 tiles and scale products of
+  // four unrolled blocks would all be live at once
 #pragma unroll 1
   for (int blk = 0; blk < kBlk; blk++) {
     i32x4_t a[2], b[2];
-    float dw[2], mw[2];
-    f32x4_t dx[2][4], sx[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int r = wm * 64 + i * 32;
-      a[i] = *reinterpret_cast<const i32x4_t *>(xq + qswz(r + fr, 2 * blk + fc));
-      // activation scales of the 16 rows this lane's outputs cover:
-      // rows r + 8q + 4 fc + (0..3), q = 0..3
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        dx[i][q] = *reinterpret_cast<const f32x4_t *>(xs + blk * kBM + r + 8 * q + 4 * fc);
-        if constexpr (DT == SWAMP_Q4_K)
-          sx[i][q] = *reinterpret_cast<const f32x4_t *>(xsum + blk * kBM + r + 8 * q + 4 * fc);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int r = wn * 64 + j * 32 + fr;
-      b[j] = *reinterpret_cast<const i32x4_t *>(wq + qswz(r, 2 * blk + fc));
-      dw[j] = wsc[blk * kBM + r];
-      if constexpr (DT == SWAMP_Q4_K) mw[j] = -wmn[blk * kBM + r];
-    }
 #pragma unroll
     for (int i = 0; i < 2; i++)
+      a[i] = *reinterpret_cast<const i32x4_t *>(xq + qswz(wm * 64 + i * 32 + fr, 2 * blk + fc));
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < 2; j++)
+      b[j] = *reinterpret_cast<const i32x4_t *>(wq + qswz(wn * 64 + j * 32 + fr, 2 * blk + fc));
+    // Operands of the two-block outer products: lane l carries row l & 31
+    // of activation tile i = l >> 5 (row wm 64 + l) and column l & 31 of
+    // weight tile j (the same column for both blocks).
+    const float dxl = xs[blk * kBM + wm * 64 + lane];
+    float sxl = 0.f;
+    if constexpr (DT == SWAMP_Q4_K) sxl = xsum[blk * kBM + wm * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int c = wn * 64 + j * 32 + fr;
+      const f32x32_t zero32 = {};
+      // d_x d_w for every element of tiles (0, j) and (1, j)
+      const f32x32_t sc = __builtin_amdgcn_mfma_f32_32x32x1f32(dxl, wsc[blk * kBM + c], zero32, 0, 0, 0);
+      // Q4_K's minimum term -dmin m * d_x sum(qx), accumulated directly
+      if constexpr (DT == SWAMP_Q4_K)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x1f32(sxl, -wmn[blk * kBM + c], acc[j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
         const i32x16_t zero = {};
-        const i32x16_t c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], zero, 0, 0, 0);
+        const i32x16_t q = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], zero, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          float t = __builtin_fmaf(float(c[e]), dx[i][e >> 2][e & 3] * dw[j], acc[i][j][e]);
-          if constexpr (DT == SWAMP_Q4_K) t = __builtin_fmaf(mw[j], sx[i][e >> 2][e & 3], t);
-          acc[i][j][e] = t;
-        }
+        for (int e = 0; e < 16; e++)
+          acc[j][16 * i + e] = __builtin_fmaf(float(q[e]), sc[16 * i + e], acc[j][16 * i + e]);
       }
+    }
   }
 }
 
@@ -293,13 +294,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
                   (DT == SWAMP_Q4_0 ? 36u : DT == SWAMP_Q8_0 ? 68u : 32u) * uint32_t(g.half) +
                   (DT == SWAMP_Q4_K ? 16u : 0u));
 
-  f32x16_t acc[2][2];
+  f32x32_t acc[2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int j = 0; j < 2; j++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    for (int e = 0; e < 32; e++) acc[j][e] = 0.f;
 
   Stage<DT> st;
   sload<DT>(st, g, kt0);
@@ -310,7 +309,10 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
     const uint8_t *cur = smem + s * stage_bytes<DT>();
     uint8_t *nxt = smem + (s ^ 1) * stage_bytes<DT>();
     const bool more = kt + 1 < kt1;
-    if (more) sload<DT>(st, g, kt + 1);
+    // unconditional (the last step reloads itself): after a conditional
+    // load the registers would merge old and new values, and the moves that
+    // merge them wait on the loads before compute can start
+    sload<DT>(st, g, more ? kt + 1 : kt);
     compute<DT>(acc, cur, wm, wn, lane);
     if (more) lstore<DT>(nxt, st, g, kt + 1);
     __syncthreads();
@@ -327,9 +329,10 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_kernel(
         const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * fc + (e & 3);
         if (m < M && n < N) {
           float *dst = y + size_t(m) * N + n;
-          if (part) part[(size_t(split) * M + m) * N + n] = acc[i][j][e];
-          else if (atomic) unsafeAtomicAdd(dst, acc[i][j][e]);
-          else *dst = acc[i][j][e];
+          const float v = acc[j][16 * i + e];
+          if (part) part[(size_t(split) * M + m) * N + n] = v;
+          else if (atomic) unsafeAtomicAdd(dst, v);
+          else *dst = v;
         }
       }
     }

@@ -541,11 +541,23 @@ __global__ void split_reduce_kernel(const float *__restrict__ part, float *__res
 }
 
 // ---- Q8_0 activation quantization ------------------------------------------
-// One wavefront quantizes two 32-element blocks (lanes 0-31, 32-63).
+// The arithmetic of one block, shared by both kernels: amax over the block,
+// d = amax / 127, q = round(v / d) clamped to [-127, 127], d stored as fp16
+// (the host quantizer's, byte for byte).
+__device__ __forceinline__ float q8_scale(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ int q8_code(float v, float d) {
+  const float id = d != 0.f ? 1.0f / d : 0.f;
+  const float q = fminf(127.f, fmaxf(-127.f, roundf(v * id)));
+  return int(q);
+}
+
+// Any alignment of dst: one element per thread, 32 lanes per block, byte
+// stores.  Also quantizes the blocks [first, n_blocks) left over by the
+// vector kernel below.
 template <bool kBf16>
 __global__ void quantize_q8_0_kernel(const void *__restrict__ src, uint8_t *__restrict__ dst,
-                                     size_t n_blocks) {
-  const size_t gid = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+                                     size_t first, size_t n_blocks) {
+  const size_t gid = first * 32 + size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const size_t blk = gid >> 5;
   const int i = int(gid & 31);
   const bool ok = blk < n_blocks;
@@ -557,10 +569,8 @@ __global__ void quantize_q8_0_kernel(const void *__restrict__ src, uint8_t *__re
   float a = fabsf(v);
 #pragma unroll
   for (int off = 16; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
-  const float d = a / 127.0f;
-  const float id = d != 0.f ? 1.0f / d : 0.f;
-  float q = roundf(v * id);
-  q = fminf(127.f, fmaxf(-127.f, q));
+  const float d = q8_scale(a);
+  const int q = q8_code(v, d);
   if (ok) {
     uint8_t *b = dst + blk * 34;
     b[2 + i] = uint8_t(int8_t(q));
@@ -569,6 +579,61 @@ __global__ void quantize_q8_0_kernel(const void *__restrict__ src, uint8_t *__re
       b[0] = uint8_t(h & 0xFF);
       b[1] = uint8_t(h >> 8);
     }
+  }
+}
+
+// 4-byte aligned dst: a wave quantizes 8 whole blocks, 4 consecutive
+// elements per lane (one 16-byte or 8-byte load), the block's amax over its
+// 8 lanes.  The wave's 8 output blocks are 272 contiguous bytes at a 4-byte
+// aligned offset (272 = 4 * 68): they are assembled in LDS with 2-byte
+// stores (a lane's 4 codes sit at 34 k + 2 + 4 j, 2 mod 4 for even blocks)
+// and written out as 68 dwords.  Only whole groups of 8 blocks come here.
+template <bool kBf16>
+__global__ void __launch_bounds__(256) quantize_q8_0_x8_kernel(const void *__restrict__ src,
+                                                               uint8_t *__restrict__ dst,
+                                                               size_t n_groups) {
+  __shared__ uint32_t stage[4][68];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const size_t grp = size_t(blockIdx.x) * 4 + size_t(w);
+  const bool ok = grp < n_groups;  // uniform per wave
+  const int k = lane >> 3, j = lane & 7;
+  // this workgroup's groups as one buffer range (out-of-range loads read 0)
+  const size_t g0 = size_t(blockIdx.x) * 4;
+  const uint32_t ebytes = kBf16 ? 2u : 4u;
+  const uint32_t range = uint32_t(min(n_groups - g0, size_t(4)) * 256u * ebytes);
+  const __amdgpu_buffer_rsrc_t r = swamp::make_rsrc(
+      static_cast<const uint8_t *>(src) + g0 * 256u * ebytes, range);
+  const uint32_t voff = (uint32_t(w) * 256u + uint32_t(lane) * 4u) * ebytes;
+  float v[4];
+  if constexpr (kBf16) {
+    typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
+    const u32x2v_t h = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+    v[0] = __uint_as_float(h[0] << 16);
+    v[1] = __uint_as_float(h[0] & 0xFFFF0000u);
+    v[2] = __uint_as_float(h[1] << 16);
+    v[3] = __uint_as_float(h[1] & 0xFFFF0000u);
+  } else {
+    const u32x4v_t a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = __uint_as_float(a[i]);
+  }
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int off = 4; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 8));
+  const float d = q8_scale(a);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) packed |= (uint32_t(q8_code(v[i], d)) & 0xFFu) << (8 * i);
+  uint16_t *st = reinterpret_cast<uint16_t *>(stage[w]);
+  const int o = 17 * k + 1 + 2 * j;  // in 2-byte units: byte 34 k + 2 + 4 j
+  st[o] = uint16_t(packed & 0xFFFFu);
+  st[o + 1] = uint16_t(packed >> 16);
+  if (j == 0) st[17 * k] = __builtin_bit_cast(uint16_t, _Float16(d));
+  __syncthreads();
+  if (ok) {
+    uint32_t *out = reinterpret_cast<uint32_t *>(dst + grp * 272u);
+    out[lane] = stage[w][lane];
+    if (lane < 4) out[64 + lane] = stage[w][64 + lane];
   }
 }
 
@@ -767,12 +832,22 @@ int swamp_launch_quantize_q8_0(const void *d_x, uint32_t x_type, void *d_q, size
                                hipStream_t s) {
   const size_t nb = n / 32;
   if (nb == 0) return SWAMP_OK;
-  const unsigned grid = unsigned((nb * 32 + 255) / 256);
-  if (x_type == SWAMP_BF16)
-    quantize_q8_0_kernel<true><<<grid, 256, 0, s>>>(d_x, static_cast<uint8_t *>(d_q), nb);
-  else if (x_type == SWAMP_F32)
-    quantize_q8_0_kernel<false><<<grid, 256, 0, s>>>(d_x, static_cast<uint8_t *>(d_q), nb);
-  else
-    return SWAMP_EDTYPE;
+  if (x_type != SWAMP_BF16 && x_type != SWAMP_F32) return SWAMP_EDTYPE;
+  const bool bf = x_type == SWAMP_BF16;
+  uint8_t *q = static_cast<uint8_t *>(d_q);
+  // whole groups of 8 blocks by the vector kernel when dst is 4-byte
+  // aligned; the rest (and any block of an unaligned dst) one element per thread
+  const size_t groups = reinterpret_cast<uintptr_t>(d_q) % 4 == 0 ? nb / 8 : 0;
+  if (groups > 0) {
+    const unsigned grid = unsigned((groups + 3) / 4);
+    if (bf) quantize_q8_0_x8_kernel<true><<<grid, 256, 0, s>>>(d_x, q, groups);
+    else quantize_q8_0_x8_kernel<false><<<grid, 256, 0, s>>>(d_x, q, groups);
+  }
+  const size_t first = groups * 8;
+  if (first < nb) {
+    const unsigned grid = unsigned(((nb - first) * 32 + 255) / 256);
+    if (bf) quantize_q8_0_kernel<true><<<grid, 256, 0, s>>>(d_x, q, first, nb);
+    else quantize_q8_0_kernel<false><<<grid, 256, 0, s>>>(d_x, q, first, nb);
+  }
   return hipGetLastError() == hipSuccess ? SWAMP_OK : SWAMP_ELAUNCH;
 }

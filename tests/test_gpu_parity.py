@@ -550,6 +550,37 @@ def test_quantize_q8_0_matches_host(pkg, torch_dev, x_type):
     assert np.array_equal(down(d_q), host)
 
 
+@pytest.mark.parametrize("x_type", [F32, BF16])
+@pytest.mark.parametrize("n_blocks,q_offset", [(1, 0), (7, 0), (13, 0), (8 * 37 + 5, 0),
+                                                (8 * 37 + 5, 2), (8 * 64, 1)])
+def test_quantize_q8_0_tails_and_alignment(pkg, torch_dev, x_type, n_blocks, q_offset):
+    """Block counts that leave a partial group of 8 (whole groups go to the
+    vector kernel, the rest one element per thread), and an output buffer
+    that is not 4-byte aligned (every block on the byte-store kernel).  The
+    input holds an all-zero block, a block of subnormal-sized values, large
+    values and ties at .5 after scaling."""
+    torch = torch_dev
+    n = 32 * n_blocks
+    x = acts(pkg, 1, n, mid=9 + n_blocks)[0].copy()
+    x[:32] = 0.0
+    if n_blocks > 2:
+        x[32:64] *= 1e-30
+        x[64:96] = np.linspace(-3e4, 3e4, 32, dtype=np.float32)
+    if x_type == BF16:
+        xb = pkg.to_bf16_bits(x)
+        x = (xb.astype(np.uint32) << 16).view(np.float32)
+        d_x = up(torch, xb.view(np.int16))
+    else:
+        d_x = up(torch, x)
+    buf = torch.full((n_blocks * 34 + 8,), 0xA5, dtype=torch.uint8, device="cuda")
+    pkg.quantize_q8_0(d_x.data_ptr(), x_type, buf.data_ptr() + q_offset, n, stream(torch))
+    torch.cuda.synchronize()
+    got = down(buf)
+    host = pkg.quantize(Q8_0, x.reshape(1, -1))
+    assert np.array_equal(got[q_offset:q_offset + n_blocks * 34], host)
+    assert np.all(got[:q_offset] == 0xA5) and np.all(got[q_offset + n_blocks * 34:] == 0xA5)
+
+
 # ------------------------------------------------------------ legacy exports
 
 def test_legacy_fused_gemv_q4k_host_pointers(pkg, orc, torch_dev):

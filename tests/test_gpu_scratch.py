@@ -144,6 +144,36 @@ def test_gemm_int8_split_repeat_bitwise(pkg, orc, torch_dev, errlog, dtype):
                 assert np.array_equal(y.view(np.uint32), first[key].view(np.uint32)), (key, rep)
 
 
+@pytest.mark.parametrize("x_type,m,rows,cols", [(BF16, 512, 6144, 4096), (BF16, 2048, 4096, 14336),
+                                                 (Q8_0, 512, 4096, 14336), (BF16, 40, 3000, 4096)])
+def test_split_sum_vector_and_scalar_bitwise(pkg, torch_dev, x_type, m, rows, cols):
+    """The K pieces' sum runs 4 elements per thread when y is 16-byte aligned
+    (and one per thread otherwise, here y one float past an aligned address):
+    both take the same additions in piece order, so y is the same bits."""
+    torch = torch_dev
+    s = torch.cuda.current_stream().cuda_stream
+    raw = weights(pkg, Q4_0, rows, cols, mid=m ^ rows)
+    x = acts(pkg, m, cols, mid=m ^ rows)
+    print(f"[gpu case] split sum {x_type} {m}x{rows}x{cols}", flush=True)
+    d_w = torch.from_numpy(raw).cuda()
+    if x_type == BF16:
+        d_x = torch.from_numpy(pkg.to_bf16_bits(x).view(np.int16)).cuda()
+    else:
+        d_f = torch.from_numpy(x).cuda()
+        d_x = torch.empty(m * cols // 32 * 34, dtype=torch.uint8, device="cuda")
+        pkg.quantize_q8_0(d_f.data_ptr(), F32, d_x.data_ptr(), m * cols, s)
+    buf = torch.full((m * rows + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    assert buf.data_ptr() % 16 == 0
+    ys = []
+    for off in (0, 1):
+        pkg.qgemm(Q4_0, d_w.data_ptr(), raw.size, d_x.data_ptr(), x_type,
+                  buf.data_ptr() + 4 * off, m, rows, cols, s)
+        torch.cuda.synchronize()
+        ys.append(buf.cpu().numpy()[off:off + m * rows].copy())
+    assert np.all(np.isfinite(ys[0]))
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
 @pytest.mark.parametrize("m,rows,cols", [(24, 33024, 1024), (64, 128256, 4096)])
 def test_gemm_small_m_single_piece(pkg, orc, torch_dev, errlog, dtype, m, rows, cols):

@@ -646,7 +646,8 @@ __global__ void __launch_bounds__(256) quantize_q8_0_x8_kernel(const void *__res
   uint32_t packed = 0;
 #pragma unroll
   for (int i = 0; i < 4; i++) packed |= (uint32_t(q8_code(v[i], d)) & 0xFFu) << (8 * i);
-  uint16_t *st = reinterpret_cast<uint16_t *>(stage[w]);
+  typedef uint16_t __attribute__((may_alias)) u16_alias_t;  // 2-byte view of the dword stage
+  u16_alias_t *st = reinterpret_cast<u16_alias_t *>(stage[w]);
   const int o = 17 * k + 1 + 2 * j;  // in 2-byte units: byte 34 k + 2 + 4 j
   st[o] = uint16_t(packed & 0xFFFFu);
   st[o + 1] = uint16_t(packed >> 16);

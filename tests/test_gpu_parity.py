@@ -581,6 +581,48 @@ def test_quantize_q8_0_tails_and_alignment(pkg, torch_dev, x_type, n_blocks, q_o
     assert np.all(got[:q_offset] == 0xA5) and np.all(got[q_offset + n_blocks * 34:] == 0xA5)
 
 
+@pytest.mark.parametrize("dtype", [Q4_0, Q8_0, Q4_K])
+def test_empty_and_zero_k_calls(pkg, torch_dev, dtype):
+    """Calls with no rows or no tokens return OK and leave y alone; calls with
+    K = 0 write the empty sums (zeros) over y, and the accumulating batched
+    form adds nothing (linear.rs:184 returns on an empty batch).  The
+    arguments are still validated first (the weight length covers the shape)."""
+    torch = torch_dev
+    s = stream(torch)
+    d_w = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    d_x = torch.ones(4096, dtype=torch.float32, device="cuda")
+    d_q = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    d_y = torch.full((64,), 7.0, dtype=torch.float32, device="cuda")
+
+    def y_is(v):
+        torch.cuda.synchronize()
+        return bool(torch.all(d_y == v).item())
+
+    wp, xp, yp = d_w.data_ptr(), d_x.data_ptr(), d_y.data_ptr()
+    wl = d_w.numel()  # enough bytes for every shape below
+    pkg.qgemv(dtype, wp, wl, xp, yp, 0, 256, s)
+    pkg.qgemv_batched(dtype, wp, wl, xp, yp, 0, 4, 256, 0, s)
+    pkg.qgemv_batched(dtype, wp, wl, xp, yp, 4, 0, 256, 0, s)
+    pkg.qgemm(dtype, wp, wl, xp, BF16, yp, 0, 8, 256, s)
+    pkg.qgemm(dtype, wp, wl, d_q.data_ptr(), Q8_0, yp, 8, 0, 256, s)
+    pkg.quantize_q8_0(xp, F32, d_q.data_ptr(), 0, s)
+    pkg.qdequant(dtype, wp, wl, yp, 0, s)
+    assert y_is(7.0)
+    pkg.qgemv_batched(dtype, wp, wl, xp, yp, 4, 8, 0, 1, s)  # accumulate over K = 0
+    assert y_is(7.0)
+    pkg.qgemv(dtype, wp, wl, xp, yp, 64, 0, s)
+    assert y_is(0.0)
+    d_y.fill_(7.0)
+    pkg.qgemv_batched(dtype, wp, wl, xp, yp, 4, 16, 0, 0, s)
+    assert y_is(0.0)
+    d_y.fill_(7.0)
+    pkg.qgemm(dtype, wp, wl, xp, BF16, yp, 8, 8, 0, s)
+    assert y_is(0.0)
+    d_y.fill_(7.0)
+    pkg.qgemm(dtype, wp, wl, d_q.data_ptr(), Q8_0, yp, 4, 16, 0, s)
+    assert y_is(0.0)
+
+
 # ------------------------------------------------------------ legacy exports
 
 def test_legacy_fused_gemv_q4k_host_pointers(pkg, orc, torch_dev):

@@ -44,7 +44,7 @@ Also reported (outside the timed steps):
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-prefill] [--no-small-batch] [--no-70b] [--cpu-threads 6,max]
-                       [--sweep] [--pmc-probe] [--pmc-gemm] [--pmc-batched N]
+                       [--sweep] [--pmc-probe] [--pmc-gemm] [--pmc-batched N] [--pmc-decode]
                        [--gemv-stages] [--gemv-fixed-cost] [--mfma-probe]
 --sweep adds one JSON line per extra workload after the main line: the
 Q4_K small batch at 2, 17, 24, 32 and 64 tokens (2 as one GEMV, 17-64 in
@@ -53,7 +53,8 @@ producers, the rest of the 70B prefill and the int8 prefill with Q4_K
 weights.  --pmc-probe runs only the dominant kernel
 and a copy of known size, for the rocprofv3 --pmc traffic measurement;
 --pmc-gemm the same for the 2048-token gate+up prefill GEMM; --pmc-batched N
-runs 5 small-batch launches of N tokens per 8B sweep matrix, for counter passes.
+runs 5 small-batch launches of N tokens per 8B sweep matrix, --pmc-decode 5
+launches of each Q4_0 decode matrix, for counter passes.
 --gemv-stages times the stages inside each 8B decode GEMV launch (stage
 stamps of libswamp_gpu_stamps.so), --gemv-fixed-cost the decode GEMV against
 row count, --mfma-probe the matrix-core issue microbenchmark; each prints
@@ -831,6 +832,10 @@ def main():
                          "shapes through each prefill route, forced with SWAMP_GEMM_ROUTE in two "
                          "child processes; one JSON line")
     ap.add_argument("--route-times", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-decode", action="store_true",
+                    help="only run 5 swamp_qgemv launches of each Q4_0 decode matrix (fp32 x) "
+                         "over the rotated weight copies, for rocprofv3 --pmc counter passes; "
+                         "no JSON")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only run 5 launches of the dominant kernel and one 256 MiB device copy "
                          "(the calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), no JSON")
@@ -954,6 +959,20 @@ def main():
             torch.cuda.synchronize()
             print(f"pmc batched: 5 x swamp_qgemv_batched {name} {rows}x{k} n_tok {n_tok}", flush=True)
             del w, x, y
+        return
+
+    if args.pmc_decode:
+        # the decode step's matrices under rocprofv3 --pmc: 5 launches of each
+        # (over the rotated weight copies), matrix after matrix, nothing else
+        for i, (name, rows, k) in enumerate(DECODE_SHAPES):
+            for it in range(5):
+                w = sets[it % args.copies][i]
+                rc = lib.swamp_qgemv(pkg.Q4_0, w.data_ptr(), w.numel(), xs[i].data_ptr(),
+                                     ys[i].data_ptr(), rows, k, s)
+                if rc != 0:
+                    raise pkg.GpuError(rc, "swamp_qgemv")
+            torch.cuda.synchronize()
+            print(f"pmc decode: 5 x swamp_qgemv Q4_0 {name} {rows}x{k}", flush=True)
         return
 
     if args.pmc_probe:
